@@ -1,0 +1,118 @@
+/*
+ * mi355x_attn.h - C ABI of the MI355X (gfx950) paged-attention library
+ * (libmi355x_attn.so, built from sglang_restomod_amd/csrc).
+ *
+ * Conventions for every entry point:
+ *   - Device pointers, element strides (in elements of the tensor's own dtype,
+ *     bytes for fp8), int sizes, float scales, and a hipStream_t passed as void*.
+ *     No torch types cross this boundary.
+ *   - The caller owns every buffer, outputs and workspaces included. Nothing
+ *     here allocates, frees or synchronises the host; every launch is enqueued
+ *     on `stream`, so the calls can be captured into a HIP graph.
+ *   - Return 0 (MA_OK) or a negative status; ma_last_error() then holds a
+ *     message for the calling thread. Stateless and thread-safe.
+ *
+ * KV addressing ("token table"): the KV caches are SGLang's flat token pools
+ * [slots, num_kv_heads, head_dim] (any row/head stride, head_dim contiguous).
+ * Token `pos` of sequence b lives in pool row
+ *     table[r * table_stride + (pos >> log2(page_size))] * page_size + (pos & (page_size - 1)),
+ *     r = row_index ? row_index[b] : b.
+ * With page_size 1, table = req_to_token and row_index = req_pool_indices this
+ * is SGLang's slot lookup; with a page table [B, max_pages] and row_index NULL it
+ * is the paged layout [pages, page_size, Hkv, D] of the reference's kernels.
+ * The table must cover every position below seq_lens[b].
+ *
+ * Score scale is softmax_scale * k_scale; outputs are multiplied by v_scale
+ * (sglang_restomod/attention/v100/tilelang/_paged_adapter.py:658,753-754).
+ * Query head h reads kv head h / (num_q_heads / num_kv_heads).
+ */
+#ifndef MI355X_ATTN_H
+#define MI355X_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MA_ABI_VERSION 1
+
+/* dtype codes */
+#define MA_DT_F16 0
+#define MA_DT_BF16 1
+#define MA_DT_E4M3 2 /* OCP e4m3fn, stored as bytes */
+#define MA_DT_E5M2 3 /* OCP e5m2, stored as bytes */
+
+/* status codes */
+#define MA_OK 0
+#define MA_EINVAL (-1)
+#define MA_ELAUNCH (-2)
+#define MA_EUNSUPPORTED (-3)
+
+/* Message for the last failing call on this thread ("" if none yet). */
+const char* ma_last_error(void);
+
+/* MA_ABI_VERSION of the loaded library. */
+int ma_abi_version(void);
+
+/* gcnArchName of the current device into buf (for load-time checks). */
+int ma_device_arch(char* buf, int len);
+
+/*
+ * Bytes of workspace the split-KV entry points need for `max_splits` splits over
+ * `num_tokens` query tokens (0 when max_splits <= 1).
+ */
+size_t ma_splitkv_workspace_bytes(int max_splits, int64_t num_tokens, int num_q_heads, int head_dim);
+
+/*
+ * Grouped split-KV decode: one query token per sequence.
+ * Replaces grouped_decode_forward (sglang_restomod/attention/v100/tilelang/
+ * _paged_adapter.py:402-486) with its partial and combine kernels
+ * (_kernels_paged_decode.py:41-312), and serves the decode that the V100
+ * backend hands to Triton at other shapes (flash_attn_v100_backend.py:1093-1115).
+ *   q   [batch, num_q_heads, head_dim], q_dtype MA_DT_F16 / MA_DT_BF16
+ *   k/v pools as above; kv_dtype = q_dtype, MA_DT_E4M3 or MA_DT_E5M2
+ *   seq_lens [batch] int32: keys of each sequence (0 gives a zero output)
+ *   sliding_window: -1 for none, else keys >= seq_len - 1 - window only
+ *   max_splits: grid size along the key axis; each sequence uses
+ *     min(max_splits, max(1, ceil(keys / min_tokens_per_split))) of them
+ *   workspace: ma_splitkv_workspace_bytes(max_splits, batch, ...) bytes
+ *   out [batch, num_q_heads, head_dim] in q_dtype
+ */
+int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
+                      const void* k_cache, const void* v_cache, int64_t kv_stride_row,
+                      int64_t kv_stride_head, int kv_dtype, const int32_t* table,
+                      int64_t table_stride, const int64_t* row_index, int page_size,
+                      const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
+                      int head_dim, int max_splits, int min_tokens_per_split, float softmax_scale,
+                      float k_scale, float v_scale, int sliding_window, void* workspace,
+                      size_t workspace_bytes, void* out, int64_t out_stride_tok,
+                      int64_t out_stride_head, void* stream);
+
+/*
+ * Grouped split-KV verify: a few query tokens per sequence (linear speculative
+ * chain), query row i of sequence b seeing keys j <= prefix_lens[b] + i when causal.
+ * Replaces the linear_verify branch of paged_forward
+ * (_paged_adapter.py:613-660) and its kernels (_kernels_paged_verify.py:52-433).
+ *   q [num_tokens, num_q_heads, head_dim]; query_start_loc [batch+1];
+ *   prefix_lens [batch] (NULL: seq_lens - query count); seq_lens [batch] total keys;
+ *   max_q_per_seq: upper bound of query tokens per sequence (<= 64)
+ *   workspace: ma_splitkv_workspace_bytes(max_splits, num_tokens, ...) bytes
+ */
+int ma_paged_verify(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
+                    int64_t num_tokens, const void* k_cache, const void* v_cache,
+                    int64_t kv_stride_row, int64_t kv_stride_head, int kv_dtype,
+                    const int32_t* table, int64_t table_stride, const int64_t* row_index,
+                    int page_size, const int32_t* seq_lens, const int32_t* query_start_loc,
+                    const int32_t* prefix_lens, int batch, int max_q_per_seq, int num_q_heads,
+                    int num_kv_heads, int head_dim, int causal, int sliding_window, int max_splits,
+                    int min_tokens_per_split, float softmax_scale, float k_scale, float v_scale,
+                    void* workspace, size_t workspace_bytes, void* out, int64_t out_stride_tok,
+                    int64_t out_stride_head, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_ATTN_H */

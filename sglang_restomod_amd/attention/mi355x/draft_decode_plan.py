@@ -1,0 +1,84 @@
+"""Planning helpers for draft decode (sglang_restomod/attention/v100/draft_decode_plan.py:42-104).
+
+A multi-step draft container hands each step a flat ``kv_indptr`` /
+``kv_indices`` pair. ``page_table_from_indices`` turns that into the page table
+plus per-row visible length the split-KV decoder takes, entirely on device (no
+host synchronisation, so it is safe inside a captured graph).
+``layer_shape_reason`` says why the decoder cannot serve a layer, or None.
+"""
+
+from __future__ import annotations
+
+import os
+from collections.abc import Mapping
+
+import torch
+
+from .backend_registry import env_flag
+
+ENV_FLAG = "SGLANG_MI355X_DRAFT_DECODE_NATIVE"
+PAGE_SIZE = 1
+SUPPORTED_HEAD_DIMS = (64, 128, 256)
+
+
+def native_enabled(env: Mapping[str, str] | None = None) -> bool:
+    source = os.environ if env is None else env
+    value = source.get(ENV_FLAG)
+    if value is None or not value.strip():
+        return True
+    return env_flag(ENV_FLAG, "1", source)
+
+
+def page_table_from_indices(
+    kv_indptr: torch.Tensor,
+    kv_indices: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    page_size: int = PAGE_SIZE,
+) -> int:
+    """Fill ``page_table[:rows]`` and ``seq_lens[:rows]``; return rows written (0 if the buffers are short).
+
+    Row ``r`` owns ``kv_indices[indptr[r]:indptr[r+1]]``; its logical page ``p``
+    is the page holding its token ``p * page_size``. Pages past the row's
+    length are written as 0. An empty index list zeroes every row.
+    """
+    rows = int(kv_indptr.numel()) - 1
+    if rows <= 0 or page_table.shape[0] < rows or seq_lens.shape[0] < rows:
+        return 0
+    if kv_indices.numel() == 0:
+        page_table[:rows].zero_()
+        seq_lens[:rows].zero_()
+        return rows
+    starts = kv_indptr[:rows].to(torch.int64)
+    lengths = kv_indptr[1:rows + 1].to(torch.int64) - starts
+    seq_lens[:rows].copy_(lengths.to(seq_lens.dtype))
+    width = page_table.shape[1]
+    first_token = torch.arange(width, dtype=torch.int64, device=kv_indices.device) * page_size
+    flat = (starts[:, None] + first_token[None, :]).clamp_(max=kv_indices.numel() - 1)
+    pages = torch.div(kv_indices[flat], page_size, rounding_mode="floor").to(torch.int32)
+    inside = first_token[None, :] < lengths[:, None]
+    page_table[:rows].copy_(torch.where(inside, pages, torch.zeros_like(pages)))
+    return rows
+
+
+def layer_shape_reason(layer) -> str | None:
+    """Why the split-KV decoder cannot serve ``layer`` (None when it can)."""
+    hq = int(getattr(layer, "tp_q_head_num", 0))
+    hkv = int(getattr(layer, "tp_k_head_num", 0))
+    qk = int(getattr(layer, "qk_head_dim", getattr(layer, "head_dim", 0)))
+    vd = int(getattr(layer, "v_head_dim", qk))
+    if hq <= 0 or hkv <= 0:
+        return "no_head_count"
+    if hq % hkv:
+        return f"gqa_ratio(h={hq},hkv={hkv})"
+    if qk != vd:
+        return f"qk_dim({qk})!=v_dim({vd})"
+    if qk not in SUPPORTED_HEAD_DIMS:
+        return f"head_dim({qk})_not_in_{SUPPORTED_HEAD_DIMS}"
+    if getattr(layer, "is_cross_attention", False):
+        return "cross_attention"
+    if getattr(layer, "logit_cap", None) not in (None, 0, 0.0):
+        return f"logit_cap({layer.logit_cap})"
+    if getattr(layer, "xai_temperature_len", 0) > 0:
+        return "xai_temperature"
+    return None

@@ -1,0 +1,278 @@
+"""Operators over the HIP library, with the reference adapter's signatures.
+
+* ``grouped_decode_forward`` - sglang_restomod/attention/v100/tilelang/_paged_adapter.py:402-486
+* ``paged_forward``          - _paged_adapter.py:567-759 (extend, and the linear-verify branch)
+
+Shapes and dtypes are validated here and raise ``ValueError`` the way the
+reference's gates do (_paged_adapter.py:417-418, 538-541). Workspaces are
+allocated by this layer (one growable buffer per device and stream, so reuse is
+ordered by the stream), never by the library. Nothing here synchronises with
+the host unless the caller leaves out a length hint the grid needs.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
+
+# Split-KV defaults: enough workgroups for 256 CUs x a few resident workgroups each,
+# and no split shorter than a few 32-token tiles per wave.
+DECODE_TARGET_WORKGROUPS = 2048
+DECODE_MIN_TOKENS_PER_SPLIT = 256
+VERIFY_MAX_Q_PER_SEQ = 64
+
+_WORKSPACES: dict = {}
+
+
+def _env_int(name: str, default: int) -> int:
+    raw = os.environ.get(name)
+    if raw is None or not raw.strip():
+        return default
+    try:
+        value = int(raw)
+    except ValueError as exc:
+        raise ValueError(f"{name} must be a positive integer") from exc
+    if value <= 0:
+        raise ValueError(f"{name} must be a positive integer")
+    return value
+
+
+def min_tokens_per_split() -> int:
+    return _env_int("SGLANG_MI355X_DECODE_TOKENS_PER_SPLIT", DECODE_MIN_TOKENS_PER_SPLIT)
+
+
+def target_workgroups() -> int:
+    return _env_int("SGLANG_MI355X_DECODE_TARGET_WORKGROUPS", DECODE_TARGET_WORKGROUPS)
+
+
+def q_dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return _lib.MA_DT_F16
+    if dtype == torch.bfloat16:
+        return _lib.MA_DT_BF16
+    raise ValueError(f"query dtype must be float16 or bfloat16, got {dtype}")
+
+
+def kv_dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float8_e4m3fn:
+        return _lib.MA_DT_E4M3
+    if dtype == torch.float8_e5m2:
+        return _lib.MA_DT_E5M2
+    return q_dtype_code(dtype)
+
+
+def kv_layout(cache: torch.Tensor, page_size: Optional[int] = None):
+    """(row_stride, head_stride, page_size, num_kv_heads, head_dim) of a token pool.
+
+    Accepts the flat pool [slots, Hkv, D] or the paged view [pages, ps, Hkv, D]
+    (whose pages must be contiguous runs of rows).
+    """
+    if cache.dim() == 3:
+        ps = 1 if page_size is None else int(page_size)
+        row, head = cache.stride(0), cache.stride(1)
+        hkv, dim = cache.shape[1], cache.shape[2]
+    elif cache.dim() == 4:
+        ps = cache.shape[1]
+        if page_size is not None and int(page_size) != ps:
+            raise ValueError(f"page_size {page_size} does not match the cache's page dim {ps}")
+        if cache.stride(0) != ps * cache.stride(1):
+            raise ValueError("paged KV cache must store each page as a contiguous run of rows")
+        row, head = cache.stride(1), cache.stride(2)
+        hkv, dim = cache.shape[2], cache.shape[3]
+    else:
+        raise ValueError(f"KV cache must be 3-D or 4-D, got shape {tuple(cache.shape)}")
+    if cache.stride(-1) != 1:
+        raise ValueError("KV cache head_dim must be contiguous")
+    if ps <= 0 or ps & (ps - 1):
+        raise ValueError(f"page size must be a power of two, got {ps}")
+    return row, head, ps, hkv, dim
+
+
+def _check_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise ValueError("the MI355X attention operators need device tensors (got a CPU tensor)")
+    for t in tensors[1:]:
+        if t is not None and t.device != dev:
+            raise ValueError("all operands must be on the same device")
+    return dev
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A growable byte buffer per (device, stream); reuse is ordered by the stream."""
+    if nbytes <= 0:
+        return None
+    key = (str(device), _stream_ptr(device))
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        cap = 1 << max(20, (nbytes - 1).bit_length())
+        buf = torch.empty(cap, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = buf
+    return buf
+
+
+def plan_splits(units: int, max_len: int, min_tokens: Optional[int] = None,
+                target: Optional[int] = None) -> int:
+    """Grid size along the key axis: enough workgroups to fill the chip, none too short."""
+    min_tokens = min_tokens or min_tokens_per_split()
+    target = target or target_workgroups()
+    by_fill = max(1, math.ceil(target / max(1, units)))
+    by_len = max(1, math.ceil(max(1, max_len) / min_tokens))
+    return max(1, min(by_fill, by_len))
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.dtype == torch.int32 and t.is_contiguous()) else t.to(torch.int32).contiguous()
+
+
+def _table(table: torch.Tensor) -> torch.Tensor:
+    if table.dtype != torch.int32:
+        raise ValueError(f"page table / req_to_token must be int32, got {table.dtype}")
+    if table.dim() != 2 or table.stride(1) != 1:
+        raise ValueError("page table must be 2-D with contiguous rows")
+    return table
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def grouped_decode_forward(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    softmax_scale: float,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+    out: Optional[torch.Tensor] = None,
+    row_index: Optional[torch.Tensor] = None,
+    page_size: Optional[int] = None,
+    sliding_window_size: int = -1,
+    max_seq_len_hint: Optional[int] = None,
+    max_splits: Optional[int] = None,
+) -> torch.Tensor:
+    """Decode one query token per sequence: ``q`` [B, Hq, D] -> [B, Hq, D] (q's dtype).
+
+    ``page_table`` [rows, width] int32 maps (row, position // page_size) to a page;
+    ``row_index`` [B] picks each sequence's row (None: row b). With page size 1
+    and ``req_to_token`` / ``req_pool_indices`` this reads SGLang's slots directly.
+    """
+    if q.dim() != 3:
+        raise ValueError(f"q must be [batch, heads, head_dim], got {tuple(q.shape)}")
+    if v_cache.dtype != k_cache.dtype:
+        raise ValueError("K and V cache dtypes must match for grouped decode.")
+    dev = _check_device(q, k_cache, v_cache, page_table, seq_lens, row_index)
+    B, Hq, D = q.shape
+    row, head, ps, Hkv, Dk = kv_layout(k_cache, page_size)
+    vrow, vhead, _, _, _ = kv_layout(v_cache, ps)
+    if (vrow, vhead) != (row, head):
+        raise ValueError("K and V caches must share one layout")
+    if Dk != D:
+        raise ValueError(f"head_dim mismatch: q {D}, cache {Dk}")
+    if Hq % Hkv:
+        raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    table = _table(page_table)
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    seq = _i32(seq_lens)
+    ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
+    max_len = int(max_seq_len_hint) if max_seq_len_hint is not None else table.shape[1] * ps
+    splits = int(max_splits) if max_splits else plan_splits(B * Hkv, max_len)
+    lib = _lib.load()
+    nbytes = lib.ma_splitkv_workspace_bytes(splits, B, Hq, D)
+    ws = workspace(dev, nbytes)
+    status = lib.ma_grouped_decode(
+        q.data_ptr(), q.stride(0), q.stride(1), q_dtype_code(q.dtype),
+        k_cache.data_ptr(), v_cache.data_ptr(), row, head, kv_dtype_code(k_cache.dtype),
+        table.data_ptr(), table.stride(0), _ptr(ridx), ps,
+        seq.data_ptr(), B, Hq, Hkv, D,
+        splits, min_tokens_per_split(), float(softmax_scale), float(k_scale), float(v_scale),
+        int(sliding_window_size), _ptr(ws), nbytes,
+        out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
+    )
+    _lib.check(status, "ma_grouped_decode")
+    return out
+
+
+def paged_verify_forward(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    query_start_loc: torch.Tensor,
+    prefix_kv_lens: Optional[torch.Tensor],
+    *,
+    max_q_per_seq: int,
+    softmax_scale: float,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+    causal: bool = True,
+    sliding_window_size: int = -1,
+    out: Optional[torch.Tensor] = None,
+    row_index: Optional[torch.Tensor] = None,
+    page_size: Optional[int] = None,
+    max_seq_len_hint: Optional[int] = None,
+    max_splits: Optional[int] = None,
+) -> torch.Tensor:
+    """Few query rows per sequence over a long prefix (linear-chain target verify)."""
+    if q.dim() != 3:
+        raise ValueError(f"q must be [tokens, heads, head_dim], got {tuple(q.shape)}")
+    if v_cache.dtype != k_cache.dtype:
+        raise ValueError("K and V cache dtypes must match")
+    dev = _check_device(q, k_cache, v_cache, block_table, seq_lens, query_start_loc)
+    T, Hq, D = q.shape
+    row, head, ps, Hkv, Dk = kv_layout(k_cache, page_size)
+    if Dk != D or Hq % Hkv:
+        raise ValueError("head shape mismatch between q and the KV cache")
+    if not 0 < max_q_per_seq <= VERIFY_MAX_Q_PER_SEQ:
+        raise ValueError(f"verify serves 1..{VERIFY_MAX_Q_PER_SEQ} query rows per sequence")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    table = _table(block_table)
+    B = seq_lens.shape[0]
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    seq = _i32(seq_lens)
+    qsl = _i32(query_start_loc)
+    pre = None if prefix_kv_lens is None else _i32(prefix_kv_lens)
+    ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
+    max_len = int(max_seq_len_hint) if max_seq_len_hint is not None else table.shape[1] * ps
+    G = Hq // Hkv
+    rows = max_q_per_seq * G
+    nb = 1 if rows <= 16 else (2 if rows <= 32 else 4)
+    row_groups = math.ceil(rows / (16 * nb))
+    splits = int(max_splits) if max_splits else plan_splits(B * Hkv * row_groups, max_len)
+    lib = _lib.load()
+    nbytes = lib.ma_splitkv_workspace_bytes(splits, T, Hq, D)
+    ws = workspace(dev, nbytes)
+    status = lib.ma_paged_verify(
+        q.data_ptr(), q.stride(0), q.stride(1), q_dtype_code(q.dtype), T,
+        k_cache.data_ptr(), v_cache.data_ptr(), row, head, kv_dtype_code(k_cache.dtype),
+        table.data_ptr(), table.stride(0), _ptr(ridx), ps,
+        seq.data_ptr(), qsl.data_ptr(), _ptr(pre),
+        B, int(max_q_per_seq), Hq, Hkv, D,
+        1 if causal else 0, int(sliding_window_size), splits, min_tokens_per_split(),
+        float(softmax_scale), float(k_scale), float(v_scale), _ptr(ws), nbytes,
+        out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
+    )
+    _lib.check(status, "ma_paged_verify")
+    return out

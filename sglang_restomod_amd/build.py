@@ -1,0 +1,79 @@
+"""Build libmi355x_attn.so in-tree from csrc/*.hip with hipcc for gfx950.
+
+    python -m sglang_restomod_amd.build        (or __graft_entry__.build())
+
+Each source compiles to an object under csrc/_build/ in parallel, then one
+hipcc link produces sglang_restomod_amd/libmi355x_attn.so. Packed fp32 VALU
+instructions are disabled for device code (-packed-fp32-ops).
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+OUT = PKG / "libmi355x_attn.so"
+ARCH = os.environ.get("MI355X_ATTN_ARCH", "gfx950")
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC)")
+
+
+def common_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wno-unused-command-line-argument",
+        f"-I{PKG.parent / 'include'}",
+    ]
+
+
+def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
+    cmd = [hipcc(), *common_flags(), *extra, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    return obj, proc.stderr
+
+
+def build(verbose: bool = False, extra: list[str] | None = None, jobs: int | None = None) -> Path:
+    """Compile every csrc/*.hip and link the shared library; returns its path."""
+    extra = list(extra or [])
+    srcs = sorted(CSRC.glob("*.hip"))
+    if not srcs:
+        raise RuntimeError(f"no sources under {CSRC}")
+    bdir = CSRC / "_build"
+    bdir.mkdir(exist_ok=True)
+    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) // 2), 8)
+    objs = []
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [ex.submit(_compile, s, bdir / (s.stem + ".o"), extra) for s in srcs]
+        for f in futs:
+            obj, err = f.result()
+            objs.append(obj)
+            if verbose and err.strip():
+                print(err, file=sys.stderr)
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,86 @@
+"""The C-ABI library: builds, loads, exports every symbol include/*.h declares, and
+rejects bad arguments before launching anything (no GPU needed for these)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = []
+    inc = os.path.join(ROOT, "include")
+    for f in sorted(os.listdir(inc)):
+        if f.endswith(".h"):
+            text = open(os.path.join(inc, f)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"\b(ma_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from sglang_restomod_amd.attention.mi355x import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared()
+    assert "ma_grouped_decode" in names and "ma_last_error" in names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+
+
+def test_python_signatures_cover_the_header():
+    from sglang_restomod_amd.attention.mi355x import _lib
+
+    assert set(_declared()) == set(_lib.SIGNATURES)
+
+
+def test_abi_version(lib):
+    hdr = open(os.path.join(ROOT, "include", "mi355x_attn.h")).read()
+    want = int(re.search(r"#define MA_ABI_VERSION (\d+)", hdr).group(1))
+    assert lib.ma_abi_version() == want
+
+
+def _decode_args(**over):
+    args = dict(q=1 << 20, qs0=1024, qs1=128, qdt=1, k=1 << 21, v=1 << 22, rs=1024, hs=128, kvdt=1,
+                table=1 << 23, tstride=64, rowidx=None, ps=1, seq=1 << 24, batch=2, hq=8, hkv=8, dim=128,
+                splits=1, mintok=256, sm=0.1, ks=1.0, vs=1.0, win=-1, ws=None, wsb=0,
+                out=1 << 25, os0=1024, os1=128, stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("over,msg", [
+    ({"dim": 96}, "head_dim"),
+    ({"qdt": 2}, "q dtype"),
+    ({"kvdt": 0}, "16-bit KV dtype must equal"),
+    ({"hq": 12, "hkv": 8}, "head counts"),
+    ({"ps": 3}, "power of two"),
+    ({"sm": 0.0}, "scale"),
+    ({"q": (1 << 20) + 2}, "aligned"),
+    ({"splits": 4, "ws": None, "wsb": 0}, "workspace"),
+])
+def test_bad_arguments_are_rejected_before_launch(lib, over, msg):
+    status = lib.ma_grouped_decode(*_decode_args(**over))
+    assert status != 0
+    assert msg in lib.ma_last_error().decode()
+
+
+def test_empty_batch_is_a_no_op(lib):
+    assert lib.ma_grouped_decode(*_decode_args(batch=0)) == 0
+
+
+def test_workspace_size_formula(lib):
+    assert lib.ma_splitkv_workspace_bytes(1, 64, 64, 128) == 0
+    n = lib.ma_splitkv_workspace_bytes(4, 64, 64, 128)
+    assert n >= 4 * 64 * 64 * 129 * 4 and n % 256 == 0
