@@ -1,0 +1,256 @@
+"""Benchmark of the MI355X paged-attention hot path on one GPU.
+
+    python bench.py [--steps K] [--warmup W] [--workload N] [--secondary] [--no-cpu-baseline]
+
+One step = one call of the hot path over one batch of synthetic input already
+resident in HBM:
+
+* workload 1 (default, the headline): batched ragged paged decode, B=64,
+  ctx U[1024, 8192], 64 q / 8 kv heads, D=128, bf16, page size 1 with shuffled
+  slots. ``value`` = algorithmic GB/s (K+V once per token and kv head, 4 B of
+  slot index per token, q in and out) over the timed region.
+* ``--secondary`` adds the other workloads (extend TFLOP/s, fp8 decode GB/s,
+  verify GB/s) as extra fields of the same JSON line.
+
+``roofline`` compares the dominant launch's algorithmic bytes / HIP-event time
+with the 8 TB/s HBM peak. ``cpu_baseline`` times the torch-native SDPA
+restatement of the same workload (per-sequence gather + fp32 SDPA) on this
+host's cores. Prints exactly one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+METRIC = "decode attn GB/s & % HBM roofline; extend attn TFLOP/s & % MFMA peak (1 GPU)"
+
+
+def _parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", type=int, default=1)
+    p.add_argument("--secondary", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=20.0)
+    return p.parse_args()
+
+
+def _runner(w):
+    """A zero-argument callable running the hot path once on workload ``w``."""
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    hint = max(w.seq_lens_cpu)
+    if w.mode == "decode":
+        out = w.q.new_empty(w.q.shape)
+        return lambda: ops.grouped_decode_forward(
+            w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, softmax_scale=w.softmax_scale,
+            k_scale=w.k_scale, v_scale=w.v_scale, out=out, row_index=w.req_pool_indices,
+            max_seq_len_hint=hint)
+    qsl = w.query_start_loc
+    T = int(w.extend_lens.max())
+    out = w.q.new_empty(w.q.shape)
+    if w.mode == "verify":
+        return lambda: ops.paged_verify_forward(
+            w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens,
+            max_q_per_seq=T, softmax_scale=w.softmax_scale, out=out, row_index=w.req_pool_indices,
+            max_seq_len_hint=hint)
+    return lambda: ops.paged_forward(
+        w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens, out=out,
+        softmax_scale=w.softmax_scale, causal=True, row_index=w.req_pool_indices,
+        max_seq_len_hint=hint, max_q_len_hint=T)
+
+
+def _time_gpu(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]  # ms, kernels of one call
+    return wall / steps * 1e3, per
+
+
+def _cpu_baseline(w, budget_s):
+    """torch-native restatement on this host's cores, on a bounded sample of sequences."""
+    import torch
+
+    from oracle import torch_native as TN
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    kc, vc = w.k_pool.cpu(), w.v_pool.cpu()
+    qc = w.q.cpu()
+    r2t, rpi = w.req_to_token.cpu(), w.req_pool_indices.cpu()
+    seq = w.seq_lens.cpu()
+    B = w.batch
+
+    def run(rows):
+        if w.mode == "decode":
+            TN.decode(qc, kc, vc, r2t, rpi, seq, softmax_scale=w.softmax_scale, k_scale=w.k_scale,
+                      v_scale=w.v_scale, batch_subset=rows)
+        else:
+            pre = w.prefix_lens.cpu().tolist()
+            ext = w.extend_lens.cpu().tolist()
+            qsl = [0]
+            for e in ext:
+                qsl.append(qsl[-1] + e)
+            sub_q = torch.cat([qc[qsl[b]:qsl[b + 1]] for b in rows])
+            TN.extend(sub_q, kc, vc, r2t, rpi[rows], [pre[b] for b in rows], [ext[b] for b in rows],
+                      softmax_scale=w.softmax_scale)
+
+    # grow the sample until one pass takes a measurable share of the budget
+    n = 1
+    t = 0.0
+    while True:
+        rows = list(range(min(n, B)))
+        t0 = time.perf_counter()
+        run(rows)
+        t = time.perf_counter() - t0
+        if n >= B or t * 3 >= budget_s / 4:
+            break
+        n = min(B, max(n + 1, int(n * max(2.0, (budget_s / 8) / max(t, 1e-3)))))
+    reps = max(1, min(3, int(budget_s / max(t, 1e-3)) - 1))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run(rows)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    frac = len(rows) / B
+    return med, frac, cores, rows
+
+
+def _workload_metrics(w):
+    from oracle import workloads
+
+    return workloads.algorithmic_bytes(w), workloads.algorithmic_flops(w)
+
+
+def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
+    import torch
+
+    from oracle import workloads
+
+    w = workloads.make(index, device=torch.device("cuda:0"), kv_format=kv_format)
+    fn = _runner(w)
+    wall_ms, per = _time_gpu(fn, steps, warmup)
+    nbytes, flops = _workload_metrics(w)
+    ev_ms = statistics.mean(per)
+    res = {
+        "workload": w.name,
+        "mode": w.mode,
+        "kv": str(w.k_pool.dtype).replace("torch.", ""),
+        "ms_per_step": wall_ms,
+        "event_ms_mean": ev_ms,
+        "event_ms_min": min(per),
+        "algorithmic_bytes": nbytes,
+        "algorithmic_flops": flops,
+        "GBps": nbytes / (ev_ms * 1e-3) / 1e9,
+        "TFLOPs": flops / (ev_ms * 1e-3) / 1e12,
+        "tokens_per_s": (w.batch if w.mode == "decode" else int(w.extend_lens.sum())) / (wall_ms * 1e-3),
+    }
+    res["hbm_frac"] = res["GBps"] / HBM_PEAK_GBS
+    res["mfma_frac"] = res["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
+    if cpu_baseline:
+        med, frac, cores, rows = _cpu_baseline(w, cpu_seconds)
+        sub_bytes = nbytes * frac if w.mode == "decode" else None
+        res["cpu"] = {
+            "seconds": med, "cores": cores, "sequences": len(rows), "of": w.batch,
+            "GBps": (nbytes * frac) / med / 1e9, "TFLOPs": (flops * frac) / med / 1e12,
+            "sample_bytes": sub_bytes,
+        }
+    del w, fn
+    torch.cuda.empty_cache()
+    return res
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(sharding across GPUs is described in DESIGN.md, not launched)"}))
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    head = _measure(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_seconds)
+    bound_hbm = head["mode"] != "extend"
+    line = {
+        "metric": METRIC,
+        "value": round(head["GBps"] if bound_hbm else head["TFLOPs"], 3),
+        "unit": "GB/s" if bound_hbm else "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if "bf16" in head["workload"] or head["kv"].startswith("float8") else "fp16",
+        "data": "synthetic (seeded N(0,1) q/k/v, shuffled token-pool slots)",
+        "config": {"workload": head["workload"], "mode": head["mode"], "kv_dtype": head["kv"],
+                   "tokens_per_s": round(head["tokens_per_s"], 1)},
+        "roofline": {
+            "bound": "hbm" if bound_hbm else "mfma",
+            "achieved": round(head["GBps"] if bound_hbm else head["TFLOPs"], 3),
+            "peak": HBM_PEAK_GBS if bound_hbm else MFMA_BF16_PEAK_TFLOPS,
+            "unit": "GB/s" if bound_hbm else "TFLOP/s",
+            "frac": round(head["hbm_frac"] if bound_hbm else head["mfma_frac"], 4),
+            "traffic": None,
+            "kernel_ms": round(head["event_ms_mean"], 5),
+            "timing": "HIP events on the launch stream around each call (split-KV partial + combine)",
+        },
+    }
+    if "cpu" in head:
+        c = head["cpu"]
+        line["cpu_baseline"] = {
+            "value": round(c["GBps"] if bound_hbm else c["TFLOPs"], 4),
+            "unit": line["unit"],
+            "cores": c["cores"],
+            "kind": "port",
+            "sample": f"torch-native SDPA restatement (per-sequence gather + fp32 SDPA) over "
+                      f"{c['sequences']} of {c['of']} sequences, median of up to 3 after a sizing pass, "
+                      f"{c['seconds']:.3f} s per pass",
+        }
+    if args.secondary:
+        sec = {}
+        for idx, fmt in ((0, None), (2, None), (3, "e4m3"), (3, "e5m2"), (4, None)):
+            if idx == args.workload:
+                continue
+            try:
+                r = _measure(idx, max(10, args.steps // 2), args.warmup, False, 0, kv_format=fmt or "e4m3")
+            except NotImplementedError as exc:
+                sec[f"w{idx}"] = {"skipped": str(exc)}
+                continue
+            key = f"w{idx}" + (f"_{fmt}" if fmt else "")
+            sec[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()
+                        if k not in ("algorithmic_bytes", "algorithmic_flops")}
+        line["secondary"] = sec
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -49,6 +49,15 @@ SIGNATURES = {
         c_float, c_float, c_float, c_void_p, c_size_t,  # scales, workspace, bytes
         c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
     ]),
+    "ma_paged_extend": (c_int, [
+        c_void_p, c_int64, c_int64, c_int, c_int64,   # q, strides, dtype, num_tokens
+        c_void_p, c_void_p, c_int64, c_int64, c_int,  # k, v, strides, kv dtype
+        c_void_p, c_int64, c_void_p, c_int,           # table, stride, row_index, page size
+        c_void_p, c_void_p, c_void_p,                 # seq_lens, qsl, prefix
+        c_int, c_int, c_int, c_int, c_int,            # batch, max_q, hq, hkv, dim
+        c_int, c_int, c_float, c_float, c_float,      # causal, window, scales
+        c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
+    ]),
 }
 
 

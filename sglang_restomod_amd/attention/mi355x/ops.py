@@ -276,3 +276,112 @@ def paged_verify_forward(
     )
     _lib.check(status, "ma_paged_verify")
     return out
+
+
+def paged_forward(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    query_start_loc: torch.Tensor,
+    prefix_kv_lens: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    block_size: Optional[int] = None,
+    num_kv_heads: Optional[int] = None,
+    softmax_scale: Optional[float] = None,
+    causal: bool = True,
+    sliding_window_size: int = -1,
+    linear_verify: bool = False,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+    max_seq_len_hint: Optional[int] = None,
+    logical_dense_kv: bool = False,
+    row_index: Optional[torch.Tensor] = None,
+    max_q_len_hint: Optional[int] = None,
+):
+    """Prefix-aware paged attention over ``q`` [num_tokens, Hq, D] (reference: paged_forward).
+
+    ``linear_verify`` routes few-row-per-sequence batches to the split-KV verifier
+    (the reference does the same, _paged_adapter.py:613-660). Returns ``out``.
+    ``logical_dense_kv`` is accepted for signature compatibility; it changes no
+    result.
+    """
+    del logical_dense_kv
+    T, Hq, D = q.shape
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    if num_kv_heads is not None:
+        hkv = kv_layout(k_cache, block_size)[3]
+        if hkv != int(num_kv_heads):
+            raise ValueError(f"num_kv_heads {num_kv_heads} does not match the cache ({hkv})")
+    B = seq_lens.shape[0]
+    if max_q_len_hint is None:
+        max_q_len_hint = int((query_start_loc[1:] - query_start_loc[:-1]).max().item()) if B else 0
+    if linear_verify and 0 < max_q_len_hint <= VERIFY_MAX_Q_PER_SEQ:
+        return paged_verify_forward(
+            q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
+            max_q_per_seq=max_q_len_hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
+            causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
+            page_size=block_size, max_seq_len_hint=max_seq_len_hint)
+    return paged_extend_forward(
+        q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
+        max_q_len=max_q_len_hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
+        causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
+        page_size=block_size)
+
+
+def paged_extend_forward(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    query_start_loc: torch.Tensor,
+    prefix_kv_lens: Optional[torch.Tensor],
+    *,
+    max_q_len: int,
+    softmax_scale: float,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+    causal: bool = True,
+    sliding_window_size: int = -1,
+    out: Optional[torch.Tensor] = None,
+    row_index: Optional[torch.Tensor] = None,
+    page_size: Optional[int] = None,
+) -> torch.Tensor:
+    """Prefix-aware extend on MFMA tiles: ``q`` [num_tokens, Hq, D] -> ``out`` (q's dtype)."""
+    if q.dim() != 3:
+        raise ValueError(f"q must be [tokens, heads, head_dim], got {tuple(q.shape)}")
+    if v_cache.dtype != k_cache.dtype:
+        raise ValueError("K and V cache dtypes must match")
+    dev = _check_device(q, k_cache, v_cache, block_table, seq_lens, query_start_loc)
+    T, Hq, D = q.shape
+    row, head, ps, Hkv, Dk = kv_layout(k_cache, page_size)
+    if kv_layout(v_cache, ps)[:2] != (row, head):
+        raise ValueError("K and V caches must share one layout")
+    if Dk != D or Hq % Hkv:
+        raise ValueError("head shape mismatch between q and the KV cache")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    table = _table(block_table)
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    B = seq_lens.shape[0]
+    seq = _i32(seq_lens)
+    qsl = _i32(query_start_loc)
+    pre = None if prefix_kv_lens is None else _i32(prefix_kv_lens)
+    ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
+    status = _lib.load().ma_paged_extend(
+        q.data_ptr(), q.stride(0), q.stride(1), q_dtype_code(q.dtype), T,
+        k_cache.data_ptr(), v_cache.data_ptr(), row, head, kv_dtype_code(k_cache.dtype),
+        table.data_ptr(), table.stride(0), _ptr(ridx), ps,
+        seq.data_ptr(), qsl.data_ptr(), _ptr(pre),
+        B, int(max_q_len), Hq, Hkv, D, 1 if causal else 0, int(sliding_window_size),
+        float(softmax_scale), float(k_scale), float(v_scale),
+        out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
+    )
+    _lib.check(status, "ma_paged_extend")
+    return out

@@ -1,0 +1,157 @@
+"""GPU parity of the MFMA extend kernel against the float64 oracle."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oracle
+from oracle import workloads
+from tests.helpers import assert_attn_close, to_f64
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    return ops
+
+
+def _gather_f64(pool, slots):
+    if pool.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+        return pool.view(torch.uint8)[slots].cpu().view(pool.dtype).float().numpy().astype(np.float64)
+    return pool[slots].float().cpu().numpy().astype(np.float64)
+
+
+def _check_rows(q, k_pool, v_pool, slots_of, prefix, qsl, out, rows_of, scale, k_scale=1.0, v_scale=1.0,
+                causal=True, window=-1, what=""):
+    """Check the listed query rows of each sequence; rows become one-row problems for the oracle."""
+    qf = to_f64(q)
+    for b, rows in rows_of.items():
+        n_total = int(prefix[b]) + (int(qsl[b + 1]) - int(qsl[b]))
+        slots = torch.as_tensor(slots_of(b, n_total), dtype=torch.int64, device=k_pool.device)
+        kb, vb = _gather_f64(k_pool, slots), _gather_f64(v_pool, slots)
+        ident = np.arange(n_total)
+        got_rows = [int(qsl[b]) + i for i in rows]
+        ref = oracle.paged_attention(
+            qf[got_rows], kb, vb, [ident] * len(rows), list(range(len(rows) + 1)),
+            [int(prefix[b]) + i for i in rows], [n_total] * len(rows),
+            softmax_scale=scale, k_scale=k_scale, v_scale=v_scale, causal=causal, sliding_window=window)
+        assert_attn_close(out[got_rows], ref, what=f"{what} seq {b} rows {rows[:3]}..")
+
+
+def _workload_extend(gpu, batch=None, scale_lens=1.0, sample=None, kv_format=None):
+    w = workloads.make(2, device=gpu, batch=batch, scale_lens=scale_lens)
+    if kv_format is not None:
+        from oracle.workloads import FP8
+
+        w.k_scale, w.v_scale = 0.75, 1.5
+        w.k_pool = (w.k_pool.float() / w.k_scale).to(FP8[kv_format])
+        w.v_pool = (w.v_pool.float() / w.v_scale).to(FP8[kv_format])
+    print(f"[case] extend {w.name} batch={w.batch} kv={w.k_pool.dtype}", flush=True)
+    qsl = w.query_start_loc
+    E = w.extend_lens.tolist()
+    out = _ops().paged_forward(
+        w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens,
+        softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale, causal=True,
+        row_index=w.req_pool_indices, max_seq_len_hint=max(w.seq_lens_cpu), max_q_len_hint=max(E))
+    torch.cuda.synchronize()
+    r2t = w.req_to_token.cpu().numpy()
+    rpi = w.req_pool_indices.cpu().numpy()
+    rows_of = {}
+    for b in range(w.batch):
+        if sample is None:
+            rows_of[b] = list(range(E[b]))
+        else:
+            rows_of[b] = sorted(set([0, 1, E[b] - 1] + list(range(0, E[b], max(1, E[b] // sample)))))
+    _check_rows(w.q, w.k_pool, w.v_pool, lambda b, n: r2t[rpi[b], :n], w.prefix_lens.tolist(),
+                qsl.tolist(), out, rows_of, w.softmax_scale, w.k_scale, w.v_scale, what=w.name)
+
+
+def test_extend_workload_small(gpu):
+    _workload_extend(gpu, batch=3, scale_lens=0.1)
+
+
+def test_extend_workload_full_sampled_rows(gpu):
+    _workload_extend(gpu, sample=12)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_extend_fp8_kv(gpu, fmt):
+    _workload_extend(gpu, batch=2, scale_lens=0.08, kv_format=fmt)
+
+
+def _synthetic(gpu, prefix, extend, heads, heads_kv, dtype=torch.bfloat16, page_size=1, seed=0, dim=128):
+    g = torch.Generator().manual_seed(seed)
+    B = len(prefix)
+    seq = [p + e for p, e in zip(prefix, extend)]
+    pages_per = [max(1, math.ceil(n / page_size)) for n in seq]
+    total_pages = sum(pages_per) + 1
+    k = torch.randn(total_pages * page_size, heads_kv, dim, generator=g).to(dtype).to(gpu)
+    v = torch.randn(total_pages * page_size, heads_kv, dim, generator=g).to(dtype).to(gpu)
+    T = sum(extend)
+    q = torch.randn(T, heads, dim, generator=g).to(dtype).to(gpu)
+    perm = (torch.randperm(total_pages - 1, generator=g) + 1).to(torch.int32)
+    table = torch.zeros(B, max(pages_per), dtype=torch.int32)
+    off = 0
+    for b, cnt in enumerate(pages_per):
+        table[b, :cnt] = perm[off:off + cnt]
+        off += cnt
+    qsl = [0]
+    for e in extend:
+        qsl.append(qsl[-1] + e)
+    return q, k, v, table, seq, qsl
+
+
+def _run_synthetic(gpu, prefix, extend, heads, heads_kv, causal=True, window=-1, dtype=torch.bfloat16,
+                   page_size=1, scale=None):
+    q, k, v, table, seq, qsl = _synthetic(gpu, prefix, extend, heads, heads_kv, dtype, page_size)
+    scale = scale or 128 ** -0.5
+    kc, vc = k, v
+    if page_size > 1:
+        kc = k.view(-1, page_size, heads_kv, 128)
+        vc = v.view(-1, page_size, heads_kv, 128)
+    out = _ops().paged_forward(
+        q, kc, vc, table.to(gpu), torch.tensor(seq, dtype=torch.int32, device=gpu),
+        torch.tensor(qsl, dtype=torch.int32, device=gpu), torch.tensor(prefix, dtype=torch.int32, device=gpu),
+        softmax_scale=scale, causal=causal, sliding_window_size=window, block_size=page_size,
+        max_q_len_hint=max(extend))
+    torch.cuda.synchronize()
+    t = table.numpy()
+    rows_of = {b: list(range(extend[b])) for b in range(len(prefix))}
+    _check_rows(q, k, v, lambda b, n: oracle.slots_from_page_table(t, b, n, page_size), prefix, qsl, out,
+                rows_of, scale, causal=causal, window=window, what=f"H{heads}/{heads_kv}")
+
+
+@pytest.mark.parametrize("heads,heads_kv", [(8, 8), (32, 8), (40, 8), (64, 8), (16, 1)])
+def test_extend_gqa_ratios(gpu, heads, heads_kv):
+    _run_synthetic(gpu, [0, 64, 300, 7], [48, 32, 129, 200], heads, heads_kv)
+
+
+def test_extend_without_prefix_and_single_tokens(gpu):
+    _run_synthetic(gpu, [0, 0, 5, 1000], [1, 2, 1, 3], 40, 8)
+
+
+def test_extend_non_causal(gpu):
+    _run_synthetic(gpu, [10, 100], [70, 33], 32, 8, causal=False)
+
+
+def test_extend_sliding_window_causal(gpu):
+    _run_synthetic(gpu, [0, 500], [300, 100], 32, 8, window=77)
+
+
+def test_extend_sliding_window_non_causal(gpu):
+    _run_synthetic(gpu, [20, 300], [40, 65], 32, 8, causal=False, window=33)
+
+
+def test_extend_fp16(gpu):
+    _run_synthetic(gpu, [64, 0], [32, 48], 32, 8, dtype=torch.float16)
+
+
+def test_extend_page_size_16_table(gpu):
+    """Reference layout [pages, 16, Hkv, D] with scattered pages (tests/test_attention_v100_gpu.py shapes)."""
+    _run_synthetic(gpu, [64, 0], [32, 48], 8, 2, dtype=torch.float16, page_size=16)
