@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 1
+#define MA_ABI_VERSION 2
 
 /* dtype codes */
 #define MA_DT_F16 0
@@ -60,10 +60,16 @@ int ma_abi_version(void);
 int ma_device_arch(char* buf, int len);
 
 /*
- * Bytes of workspace the split-KV entry points need for `max_splits` splits over
- * `num_tokens` query tokens (0 when max_splits <= 1).
+ * Number of compute units of the current device: the default persistent grid size
+ * (`num_workgroups`) of the split-KV entry points.
  */
-size_t ma_splitkv_workspace_bytes(int max_splits, int64_t num_tokens, int num_q_heads, int head_dim);
+int ma_device_workgroups(void);
+
+/*
+ * Bytes of workspace the split-KV entry points need for a persistent grid of
+ * `num_workgroups` workgroups (partial results of segments shared by two waves).
+ */
+size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim);
 
 /*
  * Grouped split-KV decode: one query token per sequence.
@@ -75,9 +81,10 @@ size_t ma_splitkv_workspace_bytes(int max_splits, int64_t num_tokens, int num_q_
  *   k/v pools as above; kv_dtype = q_dtype, MA_DT_E4M3 or MA_DT_E5M2
  *   seq_lens [batch] int32: keys of each sequence (0 gives a zero output)
  *   sliding_window: -1 for none, else keys >= seq_len - 1 - window only
- *   max_splits: grid size along the key axis; each sequence uses
- *     min(max_splits, max(1, ceil(keys / min_tokens_per_split))) of them
- *   workspace: ma_splitkv_workspace_bytes(max_splits, batch, ...) bytes
+ *   num_workgroups: persistent grid size (ma_device_workgroups() fills the chip); the
+ *     key axis of every (sequence, kv head) is cut into 32-token tiles and each wave
+ *     takes an equal contiguous share of all tiles (stream-K), so ragged lengths balance
+ *   workspace: ma_splitkv_workspace_bytes(num_workgroups, head_dim) bytes
  *   out [batch, num_q_heads, head_dim] in q_dtype
  */
 int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
@@ -85,8 +92,8 @@ int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
                       int64_t kv_stride_head, int kv_dtype, const int32_t* table,
                       int64_t table_stride, const int64_t* row_index, int page_size,
                       const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
-                      int head_dim, int max_splits, int min_tokens_per_split, float softmax_scale,
-                      float k_scale, float v_scale, int sliding_window, void* workspace,
+                      int head_dim, int num_workgroups, float softmax_scale, float k_scale,
+                      float v_scale, int sliding_window, void* workspace,
                       size_t workspace_bytes, void* out, int64_t out_stride_tok,
                       int64_t out_stride_head, void* stream);
 
@@ -98,7 +105,7 @@ int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
  *   q [num_tokens, num_q_heads, head_dim]; query_start_loc [batch+1];
  *   prefix_lens [batch] (NULL: seq_lens - query count); seq_lens [batch] total keys;
  *   max_q_per_seq: upper bound of query tokens per sequence (<= 64)
- *   workspace: ma_splitkv_workspace_bytes(max_splits, num_tokens, ...) bytes
+ *   num_workgroups / workspace: as for ma_grouped_decode
  */
 int ma_paged_verify(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
                     int64_t num_tokens, const void* k_cache, const void* v_cache,
@@ -106,8 +113,8 @@ int ma_paged_verify(const void* q, int64_t q_stride_tok, int64_t q_stride_head, 
                     const int32_t* table, int64_t table_stride, const int64_t* row_index,
                     int page_size, const int32_t* seq_lens, const int32_t* query_start_loc,
                     const int32_t* prefix_lens, int batch, int max_q_per_seq, int num_q_heads,
-                    int num_kv_heads, int head_dim, int causal, int sliding_window, int max_splits,
-                    int min_tokens_per_split, float softmax_scale, float k_scale, float v_scale,
+                    int num_kv_heads, int head_dim, int causal, int sliding_window,
+                    int num_workgroups, float softmax_scale, float k_scale, float v_scale,
                     void* workspace, size_t workspace_bytes, void* out, int64_t out_stride_tok,
                     int64_t out_stride_head, void* stream);
 

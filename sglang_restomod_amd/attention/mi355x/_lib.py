@@ -29,13 +29,14 @@ SIGNATURES = {
     "ma_last_error": (c_char_p, []),
     "ma_abi_version": (c_int, []),
     "ma_device_arch": (c_int, [c_char_p, c_int]),
-    "ma_splitkv_workspace_bytes": (c_size_t, [c_int, c_int64, c_int, c_int]),
+    "ma_device_workgroups": (c_int, []),
+    "ma_splitkv_workspace_bytes": (c_size_t, [c_int, c_int]),
     "ma_grouped_decode": (c_int, [
         c_void_p, c_int64, c_int64, c_int,            # q, strides, dtype
         c_void_p, c_void_p, c_int64, c_int64, c_int,  # k, v, row/head stride, kv dtype
         c_void_p, c_int64, c_void_p, c_int,           # table, stride, row_index, page size
         c_void_p, c_int, c_int, c_int, c_int,         # seq_lens, batch, hq, hkv, dim
-        c_int, c_int, c_float, c_float, c_float,      # max_splits, min_tokens, scales
+        c_int, c_float, c_float, c_float,             # num_workgroups, scales
         c_int, c_void_p, c_size_t,                    # window, workspace, bytes
         c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
     ]),
@@ -45,7 +46,7 @@ SIGNATURES = {
         c_void_p, c_int64, c_void_p, c_int,           # table, stride, row_index, page size
         c_void_p, c_void_p, c_void_p,                 # seq_lens, qsl, prefix
         c_int, c_int, c_int, c_int, c_int,            # batch, max_q, hq, hkv, dim
-        c_int, c_int, c_int, c_int,                   # causal, window, max_splits, min_tokens
+        c_int, c_int, c_int,                          # causal, window, num_workgroups
         c_float, c_float, c_float, c_void_p, c_size_t,  # scales, workspace, bytes
         c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
     ]),

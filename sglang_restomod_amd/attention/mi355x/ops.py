@@ -22,13 +22,10 @@ from . import _lib
 
 FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 
-# Split-KV defaults: enough workgroups for 256 CUs x a few resident workgroups each,
-# and no split shorter than a few 32-token tiles per wave.
-DECODE_TARGET_WORKGROUPS = 2048
-DECODE_MIN_TOKENS_PER_SPLIT = 256
 VERIFY_MAX_Q_PER_SEQ = 64
 
 _WORKSPACES: dict = {}
+_DEVICE_WORKGROUPS: dict = {}
 
 
 def _env_int(name: str, default: int) -> int:
@@ -44,12 +41,18 @@ def _env_int(name: str, default: int) -> int:
     return value
 
 
-def min_tokens_per_split() -> int:
-    return _env_int("SGLANG_MI355X_DECODE_TOKENS_PER_SPLIT", DECODE_MIN_TOKENS_PER_SPLIT)
-
-
-def target_workgroups() -> int:
-    return _env_int("SGLANG_MI355X_DECODE_TARGET_WORKGROUPS", DECODE_TARGET_WORKGROUPS)
+def splitkv_workgroups(device: torch.device) -> int:
+    """Persistent grid size of the split-KV kernels: one workgroup per compute unit
+    (``SGLANG_MI355X_SPLITKV_WORKGROUPS`` overrides)."""
+    key = str(device)
+    n = _DEVICE_WORKGROUPS.get(key)
+    if n is None:
+        with torch.cuda.device(device):
+            n = int(_lib.load().ma_device_workgroups())
+        if n <= 0:
+            raise RuntimeError("could not query the device's compute-unit count")
+        _DEVICE_WORKGROUPS[key] = n
+    return _env_int("SGLANG_MI355X_SPLITKV_WORKGROUPS", n)
 
 
 def q_dtype_code(dtype: torch.dtype) -> int:
@@ -122,16 +125,6 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
-def plan_splits(units: int, max_len: int, min_tokens: Optional[int] = None,
-                target: Optional[int] = None) -> int:
-    """Grid size along the key axis: enough workgroups to fill the chip, none too short."""
-    min_tokens = min_tokens or min_tokens_per_split()
-    target = target or target_workgroups()
-    by_fill = max(1, math.ceil(target / max(1, units)))
-    by_len = max(1, math.ceil(max(1, max_len) / min_tokens))
-    return max(1, min(by_fill, by_len))
-
-
 def _i32(t: torch.Tensor) -> torch.Tensor:
     return t if (t.dtype == torch.int32 and t.is_contiguous()) else t.to(torch.int32).contiguous()
 
@@ -163,7 +156,7 @@ def grouped_decode_forward(
     page_size: Optional[int] = None,
     sliding_window_size: int = -1,
     max_seq_len_hint: Optional[int] = None,
-    max_splits: Optional[int] = None,
+    num_workgroups: Optional[int] = None,
 ) -> torch.Tensor:
     """Decode one query token per sequence: ``q`` [B, Hq, D] -> [B, Hq, D] (q's dtype).
 
@@ -194,17 +187,17 @@ def grouped_decode_forward(
         raise ValueError("out must match q's shape and dtype")
     seq = _i32(seq_lens)
     ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
-    max_len = int(max_seq_len_hint) if max_seq_len_hint is not None else table.shape[1] * ps
-    splits = int(max_splits) if max_splits else plan_splits(B * Hkv, max_len)
+    del max_seq_len_hint  # the persistent grid does not depend on lengths
+    nwg = int(num_workgroups) if num_workgroups else splitkv_workgroups(dev)
     lib = _lib.load()
-    nbytes = lib.ma_splitkv_workspace_bytes(splits, B, Hq, D)
+    nbytes = lib.ma_splitkv_workspace_bytes(nwg, D)
     ws = workspace(dev, nbytes)
     status = lib.ma_grouped_decode(
         q.data_ptr(), q.stride(0), q.stride(1), q_dtype_code(q.dtype),
         k_cache.data_ptr(), v_cache.data_ptr(), row, head, kv_dtype_code(k_cache.dtype),
         table.data_ptr(), table.stride(0), _ptr(ridx), ps,
         seq.data_ptr(), B, Hq, Hkv, D,
-        splits, min_tokens_per_split(), float(softmax_scale), float(k_scale), float(v_scale),
+        nwg, float(softmax_scale), float(k_scale), float(v_scale),
         int(sliding_window_size), _ptr(ws), nbytes,
         out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
     )
@@ -231,7 +224,7 @@ def paged_verify_forward(
     row_index: Optional[torch.Tensor] = None,
     page_size: Optional[int] = None,
     max_seq_len_hint: Optional[int] = None,
-    max_splits: Optional[int] = None,
+    num_workgroups: Optional[int] = None,
 ) -> torch.Tensor:
     """Few query rows per sequence over a long prefix (linear-chain target verify)."""
     if q.dim() != 3:
@@ -255,14 +248,10 @@ def paged_verify_forward(
     qsl = _i32(query_start_loc)
     pre = None if prefix_kv_lens is None else _i32(prefix_kv_lens)
     ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
-    max_len = int(max_seq_len_hint) if max_seq_len_hint is not None else table.shape[1] * ps
-    G = Hq // Hkv
-    rows = max_q_per_seq * G
-    nb = 1 if rows <= 16 else (2 if rows <= 32 else 4)
-    row_groups = math.ceil(rows / (16 * nb))
-    splits = int(max_splits) if max_splits else plan_splits(B * Hkv * row_groups, max_len)
+    del max_seq_len_hint
+    nwg = int(num_workgroups) if num_workgroups else splitkv_workgroups(dev)
     lib = _lib.load()
-    nbytes = lib.ma_splitkv_workspace_bytes(splits, T, Hq, D)
+    nbytes = lib.ma_splitkv_workspace_bytes(nwg, D)
     ws = workspace(dev, nbytes)
     status = lib.ma_paged_verify(
         q.data_ptr(), q.stride(0), q.stride(1), q_dtype_code(q.dtype), T,
@@ -270,7 +259,7 @@ def paged_verify_forward(
         table.data_ptr(), table.stride(0), _ptr(ridx), ps,
         seq.data_ptr(), qsl.data_ptr(), _ptr(pre),
         B, int(max_q_per_seq), Hq, Hkv, D,
-        1 if causal else 0, int(sliding_window_size), splits, min_tokens_per_split(),
+        1 if causal else 0, int(sliding_window_size), nwg,
         float(softmax_scale), float(k_scale), float(v_scale), _ptr(ws), nbytes,
         out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
     )

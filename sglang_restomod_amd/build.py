@@ -33,7 +33,7 @@ def common_flags() -> list[str]:
     return [
         f"--offload-arch={ARCH}",
         "-O3",
-        "-std=c++17",
+        "-std=c++20",
         "-fPIC",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
@@ -49,8 +49,24 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
     return obj, proc.stderr
 
 
+def verify_inflight(src: Path, extra: list[str]) -> int:
+    """Generate the device assembly of `src` and count in-flight register hazards."""
+    from . import isa_check
+
+    asm = CSRC / "_build" / (src.stem + ".s")
+    cmd = [hipcc(), *common_flags(), *extra, "-S", "--cuda-device-only", str(src), "-o", str(asm)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"assembly generation failed: {' '.join(cmd)}\n{proc.stderr}")
+    return isa_check.check_file(str(asm))
+
+
 def build(verbose: bool = False, extra: list[str] | None = None, jobs: int | None = None) -> Path:
-    """Compile every csrc/*.hip and link the shared library; returns its path."""
+    """Compile every csrc/*.hip and link the shared library; returns its path.
+
+    Sources whose kernels issue loads as inline assembly (marked `MA_ASM_PIPELINE`) are
+    also checked for in-flight register hazards; any hazard fails the build.
+    """
     extra = list(extra or [])
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
@@ -66,6 +82,12 @@ def build(verbose: bool = False, extra: list[str] | None = None, jobs: int | Non
             objs.append(obj)
             if verbose and err.strip():
                 print(err, file=sys.stderr)
+    for src in srcs:
+        if "MA_ASM_PIPELINE" in src.read_text():
+            hazards = verify_inflight(src, extra)
+            if hazards:
+                raise RuntimeError(f"{src.name}: {hazards} in-flight register hazards in the generated code "
+                                   "(python -m sglang_restomod_amd.isa_check on csrc/_build/*.s lists them)")
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

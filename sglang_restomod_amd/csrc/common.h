@@ -16,6 +16,32 @@ typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
+
+// Global-memory pointers. Pointers that reach a kernel inside a by-value argument
+// struct are generic (flat) to the compiler; casting them to address space 1 makes
+// it emit global_load/global_store, whose completion counts stay exact (flat accesses
+// count against both the vector-memory and the LDS counters and make every wait
+// conservative).
+#define MA_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const T MA_GLOBAL* gptr(const T* p) {
+  return (const T MA_GLOBAL*)p;
+}
+template <typename T>
+__device__ __forceinline__ T MA_GLOBAL* gptr_mut(T* p) {
+  return (T MA_GLOBAL*)p;
+}
+
+// Read-only metadata indexed by a wave-uniform value: through the constant address
+// space the compiler can use scalar loads, which complete on the LDS/scalar counter and
+// never wait behind in-flight vector loads.
+#define MA_CONST __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ const T MA_CONST* cptr(const T* p) {
+  return (const T MA_CONST*)p;
+}
 
 // dtype codes shared with the C ABI (include/mi355x_attn.h)
 enum DType : int { DT_F16 = 0, DT_BF16 = 1, DT_E4M3 = 2, DT_E5M2 = 3 };
@@ -168,7 +194,7 @@ struct TokenTable {
 };
 
 __device__ __forceinline__ int64_t kv_row(const TokenTable& t, int64_t seq_row, int pos) {
-  const int32_t page = t.table[seq_row * t.stride + (pos >> t.page_shift)];
+  const int32_t page = gptr(t.table)[seq_row * t.stride + (pos >> t.page_shift)];
   return ((int64_t)page << t.page_shift) | (int64_t)(pos & ((1 << t.page_shift) - 1));
 }
 

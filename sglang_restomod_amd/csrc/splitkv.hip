@@ -1,40 +1,52 @@
-// Grouped split-KV attention for few query rows per sequence: decode (one row)
-// and linear-chain target verify (a handful of draft rows under a causal mask).
+// Grouped split-KV attention for few query rows per sequence: decode (one row) and
+// linear-chain target verify (a handful of draft rows under a causal mask).
 //
 // Replaces the reference's grouped decode partial + combine
-// (sglang_restomod/attention/v100/tilelang/_kernels_paged_decode.py:41-312) and
-// the grouped verify partial + combine (_kernels_paged_verify.py:52-433).
+// (sglang_restomod/attention/v100/tilelang/_kernels_paged_decode.py:41-312) and the
+// grouped verify partial + combine (_kernels_paged_verify.py:52-433).
 //
-// Work decomposition (one workgroup = 4 waves):
-//   blockIdx.x = kv_head * row_groups + row_group,  blockIdx.y = split,  blockIdx.z = sequence.
-//   A row group is 16*NB query rows of one kv head: row R -> (query token R / G, head R % G),
-//   so every GQA head of a kv head is served from one read of its K/V.
-//   The split's key range is cut into 32-token tiles; wave w takes tiles w, w+4, ...
-//   Each wave keeps its own online-softmax state; the four are merged in LDS at the end.
+// Work decomposition (stream-K): the key axis of every (sequence, kv head, row group)
+// "segment" is cut into 32-token tiles. All tiles of all segments form one list, and a
+// persistent grid (one 4-wave workgroup per CU) hands every wave an equal, contiguous
+// range of that list. A wave walks its range, keeps an online-softmax state per segment
+// piece, writes the output directly when it covered a whole segment and a partial
+// (normalised O + log2 LSE) when the segment continues in a neighbouring wave's range.
+// A second kernel merges the partials of split segments. Ragged lengths therefore cost
+// nothing in balance, and the number of partials is at most two per wave.
 //
-// Per 32-token tile and wave (all MFMA 16x16x32, fp32 accumulate):
-//   S^T[t, r] = K[t, :] . Q[r, :]     M = tokens (two 16-token blocks), N = rows, K = head dim.
-//               K rows are loaded from HBM straight into the A-operand layout (16 B per lane
-//               per step); Q^T sits in registers for the whole kernel.
-//   O^T[d, r] += V^T[d, t] P^T[t, r]  M = head dim (16 per step), N = rows, K = 32 tokens.
-//               The S^T accumulator already holds, per lane, the 8 tokens the P^T B-operand
-//               needs (tokens 4j..4j+3 and 16+4j..16+4j+3 of lane group j), so P never moves
-//               between lanes. V is transposed through a per-wave LDS tile whose rows are
-//               head-dim entries and whose 32 columns are the tokens in that same order.
-//   16-bit V: P is split into bf16/fp16 hi + lo halves (two MFMAs) for bf16, or cast to fp16.
-//   fp8 V: dequantized to fp16 in registers, P cast to fp16.
+// A row group is 16*NB query rows of one kv head: row R -> (query token R / G,
+// GQA head R % G), so every head of a kv head is served from one read of its K/V.
 //
-// Numerics: scores and softmax in fp32 (exp2 domain, scale folded in), partial outputs and
-// LSE (log2 domain, -2^30 for an empty split) in fp32, output in the query dtype.
+// Per 32-token tile (MFMA 16x16x32, fp32 accumulate):
+//   S^T[t, r] = K[t, :] . Q[r, :]     A = K rows straight from HBM in operand layout,
+//                                     B = Q^T (registers, reloaded per segment).
+//   O^T[d, r] += V^T[d, t] P^T[t, r]  P^T comes straight from the S^T accumulators; V is
+//                                     written row-major into a per-wave LDS tile and read
+//                                     back transposed (ds_read_b64_tr_b16 / _tr_b8).
+//   bf16 V: P split into two bf16 halves (exact to ~16 bits); fp16 / fp8 V: fp16 P.
+//
+// Memory pipeline: K and V of the next S-1 tiles are in flight while a tile computes
+// (S = 5 for 16-bit KV, 8 for fp8: about 250 KB per CU, which is what random 256-byte
+// row gathers need to approach HBM bandwidth). K rows land in a register ring in MFMA
+// operand layout; V rows go straight to a per-wave LDS ring by DMA (global_load_lds),
+// issued before the tile's K loads so that the compiler's wait for the K registers also
+// covers them. Slots are looked up 2S-3 tiles ahead of compute. The issue cursor clamps
+// at the wave's last tile, so the pipelined loop has no data-dependent branches around
+// loads and the compiler's wait counts stay exact.
+
+#include <type_traits>
 
 #include "common.h"
+
+// MA_ASM_PIPELINE: the build verifies the generated code of this file for accesses to
+// registers whose inline-assembly loads are still in flight.
 #include "capi_internal.h"
 
 namespace ma {
 
 constexpr int kWaves = 4;
 constexpr int kTile = 32;
-constexpr int kVtRow = 80;  // bytes per head-dim row of the V^T tile: 32 tokens * 2 B + 16 B pad
+constexpr int kMaxRows = 32;  // 16 * NB, NB <= 2
 
 struct SplitKVArgs {
   const void* q;
@@ -46,206 +58,363 @@ struct SplitKVArgs {
   const int64_t* row_index;  // request row of each sequence, or null (row b)
   const int32_t* seq_lens;   // keys visible to the last query row of each sequence
   const int32_t* qsl;        // [B+1] query start per sequence, or null (one row per sequence)
-  const int32_t* prefix;     // [B] cached prefix per sequence, or null (seq_len - 1)
+  const int32_t* prefix;     // [B] cached prefix per sequence, or null (seq_len - query count)
   int batch, hq, hkv, group;
-  int row_groups;
-  int max_splits, min_tokens;
+  int row_groups;            // row groups per (sequence, kv head) in the largest sequence
+  int rows;                  // rows per row group (16 * NB)
   int causal, window;
-  float scale_log2;  // softmax_scale * k_scale * log2(e)
+  float scale_log2;          // softmax_scale * k_scale * log2(e)
   float v_scale;
-  float* part_o;     // [max_splits][qrows][D]
-  float* part_lse;   // [max_splits][qrows]
-  int64_t qrows;     // total query rows (tokens * hq)
+  int nwaves;                // waves of the persistent grid
+  float* part_o;             // [nwaves][2][kMaxRows][D]
+  float* part_lse;           // [nwaves][2][kMaxRows]
   void* out;
   int64_t out_stride_tok, out_stride_head;
 };
 
-struct SeqInfo {
-  int seq, prefix, tok0, ntok, lo_min, span, active, split_len;
+// Geometry of one sequence; identical in the partial and the combine kernel.
+struct Geom {
+  int b, seq, ntok, prefix, tok0, lo_min, span, nt, rg_real;
+  int64_t seq_row;
 };
 
-// Identical in the partial and the combine kernel: the combine re-derives how many
-// splits a sequence used from its lengths alone (no extra metadata, graph-safe).
-__device__ __forceinline__ SeqInfo seq_info(const SplitKVArgs& a, int b) {
-  SeqInfo s;
-  s.seq = a.seq_lens[b];
+// Loads go through the constant address space: with a wave-uniform `b` they become
+// scalar loads (geom_u), with a per-lane `b` vector loads (scan over sequences).
+__device__ __forceinline__ Geom geom(const SplitKVArgs& a, int b) {
+  Geom g;
+  g.b = b;
+  g.seq = max(cptr(a.seq_lens)[b], 0);
   if (a.qsl) {
-    s.tok0 = a.qsl[b];
-    s.ntok = a.qsl[b + 1] - s.tok0;
-    s.prefix = a.prefix ? a.prefix[b] : s.seq - s.ntok;
+    g.tok0 = cptr(a.qsl)[b];
+    g.ntok = cptr(a.qsl)[b + 1] - g.tok0;
+    g.prefix = a.prefix ? cptr(a.prefix)[b] : g.seq - g.ntok;
   } else {
-    s.tok0 = b;
-    s.ntok = 1;
-    s.prefix = s.seq - 1;
+    g.tok0 = b;
+    g.ntok = 1;
+    g.prefix = g.seq - 1;
   }
-  s.lo_min = a.window >= 0 ? max(0, s.prefix - a.window) : 0;
-  s.lo_min = min(s.lo_min, max(s.seq, 0));
-  s.span = max(s.seq - s.lo_min, 0);
-  int want = (s.span + a.min_tokens - 1) / a.min_tokens;
-  s.active = min(a.max_splits, max(1, want));
-  s.split_len = (s.span + s.active - 1) / s.active;
-  return s;
+  g.lo_min = a.window >= 0 ? max(0, g.prefix - a.window) : 0;
+  g.lo_min = min(g.lo_min, g.seq);
+  g.span = g.seq - g.lo_min;
+  g.nt = (g.span + kTile - 1) / kTile;
+  const int real_rows = max(g.ntok, 0) * a.group;
+  g.rg_real = min(a.row_groups, (real_rows + a.rows - 1) / a.rows);
+  g.seq_row = a.row_index ? cptr(a.row_index)[b] : (int64_t)b;
+  return g;
+}
+
+__device__ __forceinline__ Geom geom_u(const SplitKVArgs& a, int b) {
+  return geom(a, __builtin_amdgcn_readfirstlane(b));
+}
+
+// tiles of sequence b over all its kv heads and row groups
+__device__ __forceinline__ int seq_work(const SplitKVArgs& a, int b) {
+  const Geom g = geom(a, b);
+  return g.nt * g.rg_real * a.hkv;
+}
+
+__device__ __forceinline__ int shfl_up_i(int v, int delta) {
+  const int lane = lane_id();
+  const int src = lane >= delta ? lane - delta : lane;
+  return __builtin_amdgcn_ds_bpermute(src << 2, v);
+}
+
+// Total tiles, and (when t >= 0) the sequence holding global tile t and t's offset in it.
+__device__ __forceinline__ void scan_work(const SplitKVArgs& a, int64_t t, int64_t& total, int& b_at, int& off_at) {
+  const int lane = lane_id();
+  int64_t base = 0;
+  b_at = -1;
+  off_at = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int b = b0 + lane;
+    const int w = b < a.batch ? seq_work(a, b) : 0;
+    int inc = w;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const int y = shfl_up_i(inc, m);
+      if (lane >= m) inc += y;
+    }
+    const int chunk = __builtin_amdgcn_readlane(inc, 63);
+    if (b_at < 0 && t >= 0 && base + chunk > t) {
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(base + inc > t);
+      const int L = __builtin_ctzll(hit);
+      b_at = b0 + L;
+      off_at = (int)(t - (base + __builtin_amdgcn_readlane(inc - w, L)));
+    }
+    base += chunk;
+  }
+  total = base;
+}
+
+// Position of a wave in its tile range: sequence geometry, kv head, row group, tile.
+struct Cursor {
+  Geom g;
+  int h, rg, tile;
+  int t;  // wave-local tile number
+};
+
+__device__ __forceinline__ void cursor_at(const SplitKVArgs& a, Cursor& c, int b, int off) {
+  c.g = geom_u(a, b);
+  const int per_seg = c.g.nt;
+  const int seg = off / per_seg;
+  c.tile = off - seg * per_seg;
+  c.h = seg / c.g.rg_real;
+  c.rg = seg - c.h * c.g.rg_real;
+  c.t = 0;
+}
+
+// Next tile of the range; stays on the last tile once the range is exhausted.
+__device__ __forceinline__ void cursor_next(const SplitKVArgs& a, Cursor& c, int count) {
+  if (c.t + 1 >= count) return;
+  ++c.t;
+  if (++c.tile < c.g.nt) return;
+  c.tile = 0;
+  if (++c.rg < c.g.rg_real) return;
+  c.rg = 0;
+  if (++c.h < a.hkv) return;
+  c.h = 0;
+  int b = c.g.b;
+  do {
+    ++b;
+    c.g = geom_u(a, b);
+  } while (c.g.nt * c.g.rg_real == 0);
 }
 
 template <bool BF16>
-__device__ __forceinline__ void store_out(void* out, int64_t off, float x) {
-  reinterpret_cast<uint16_t*>(out)[off] = f2h<BF16>(x);
+__device__ __forceinline__ u32x2 pack4(f32x4 v, float s) {
+  u32x2 pk;
+  pk[0] = (uint32_t)f2h<BF16>(v[0] * s) | ((uint32_t)f2h<BF16>(v[1] * s) << 16);
+  pk[1] = (uint32_t)f2h<BF16>(v[2] * s) | ((uint32_t)f2h<BF16>(v[3] * s) << 16);
+  return pk;
 }
 
+// Wave index holding global tile t in a grid of nw waves over `total` tiles.
+__device__ __forceinline__ int wave_of(int64_t t, int64_t total, int nw) {
+  return (int)(((t + 1) * nw - 1) / total);
+}
+__device__ __forceinline__ int64_t wave_begin(int w, int64_t total, int nw) { return (int64_t)w * total / nw; }
+
 // ---------------------------------------------------------------------------
-// Partial kernel.
-//   D: head dim (multiple of 64). NB: 16-row blocks per workgroup.
-//   QBF16: query (and 16-bit KV) is bf16. KV: DT_F16 / DT_BF16 / DT_E4M3 / DT_E5M2.
+// Partial kernel (persistent).
 // ---------------------------------------------------------------------------
 template <int D, int NB, bool QBF16, int KV>
-__global__ __launch_bounds__(256) void splitkv_partial(const SplitKVArgs a) {
+__global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args) {
+  // A local copy: the lambdas below capture by reference, and a reference to the kernel
+  // argument itself would force it into scratch memory.
+  const SplitKVArgs a = args;
+  static_assert(D == 128, "head dim 128");
   constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
-  constexpr int KK = D / 32;        // QK MFMA steps (32 head-dim entries each)
-  constexpr int DB = D / 16;        // PV MFMA steps (16 head-dim rows each)
-  constexpr int DQ = D / 4;         // head-dim entries owned by one lane group in QK
+  // pipeline stages: K of S tiles in a register ring, V of S tiles in an LDS ring
+  // (S * 8 KB per wave for 16-bit KV, S * 4 KB for fp8). Each step issues OPS vector
+  // memory instructions (one slot lookup, the V DMA, the K loads); a wave can have at
+  // most 63 outstanding, which bounds S.
+  constexpr int S = kFp8 ? 8 : 4;
+  constexpr int A = 2 * S - 3;  // slots are looked up A tiles ahead of compute
+  constexpr int KK = D / 32;          // QK MFMA steps
+  constexpr int DB = D / 16;          // PV MFMA steps
+  constexpr int DQ = D / 4;           // head-dim entries per lane group in QK
   constexpr int kRows = 16 * NB;
-  // fp8 V is dequantized to fp16 and multiplied with fp16 P; bf16 V keeps bf16 and
-  // multiplies P split in two bf16 halves.
   constexpr bool kPvBf16 = (!kFp8) && QBF16;
   constexpr bool kSplitP = kPvBf16;
+  constexpr int kElt = kFp8 ? 1 : 2;
+  constexpr int kRowB = D * kElt;           // bytes of one head row
+  constexpr int kStage = kTile * kRowB;     // bytes of one V tile
+  constexpr int kVL = kStage / 1024;        // 16-byte V loads per lane per tile
+  constexpr int KR = kFp8 ? KK / 2 : KK;    // 16-byte K loads per lane per 16-token block
+  constexpr int OPS = 1 + kVL + 2 * KR;     // vector memory instructions per pipeline step
+  static_assert((S - 1) * OPS <= 63, "more outstanding loads than the counter holds");
 
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kWaves * D * kVtRow];
-  __shared__ float sm_m[kWaves][kRows];
-  __shared__ float sm_l[kWaves][kRows];
+  __shared__ __attribute__((aligned(16))) unsigned char vring[kWaves][S][kStage];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
   const int j = lane >> 4;
+  const int W = blockIdx.x * kWaves + wave;
 
-  const int h = blockIdx.x / a.row_groups;
-  const int rg = blockIdx.x - h * a.row_groups;
-  const int split = blockIdx.y;
-  const int b = blockIdx.z;
+  int64_t total;
+  int b0, off0, bd, od;
+  scan_work(a, -1, total, bd, od);
+  const int64_t t0 = wave_begin(W, total, a.nwaves);
+  const int count = (int)(wave_begin(W + 1, total, a.nwaves) - t0);
+  if (count <= 0) return;
+  scan_work(a, t0, total, b0, off0);
 
-  const SeqInfo si = seq_info(a, b);
-  if (split >= si.active) return;
-  const int s0 = si.lo_min + split * si.split_len;
-  const int s1 = min(si.lo_min + si.span, s0 + si.split_len);
-  const int64_t seq_row = a.row_index ? a.row_index[b] : (int64_t)b;
+  const unsigned char MA_GLOBAL* kbase = gptr(reinterpret_cast<const unsigned char*>(a.k));
+  const unsigned char MA_GLOBAL* vbase = gptr(reinterpret_cast<const unsigned char*>(a.v));
+  const int64_t row_bytes = a.kv_stride_row * kElt;
+  const int64_t head_bytes = a.kv_stride_head * kElt;
 
-  // ---- this lane's query row in each 16-row block: bounds and Q^T operand ----
+  auto swz = [](int t) -> int { return kFp8 ? ((t & 3) | ((t >> 2) & 4)) : ((2 * t) & 15); };
+
+  // ---- per-tile K register ring (V goes to the LDS ring by DMA) ----
+  struct Raw {
+    u32x4 k[2][KR];
+  };
+  Raw ring[S];
+  int sreg[S];
+
+  // The pipeline's vector memory instructions are issued as inline assembly and waited
+  // for with explicit counts (wait_vm below): the compiler's own wait insertion cannot
+  // follow data across the register ring and the loop back edge, and it drains all
+  // outstanding loads before any LDS read once it has seen an LDS DMA. K rows load
+  // straight into AGPRs (MFMA operands), which the register allocator has no reason to
+  // copy before the wait; the build checks the generated code for any access to a
+  // register whose load is still in flight.
+  auto load_slot = [&](const Cursor& cu) __attribute__((always_inline)) -> int {
+    const int key0 = cu.g.lo_min + cu.tile * kTile;
+    const int pos = min(key0 + (lane & 31), cu.g.seq - 1);
+    const int32_t MA_GLOBAL* tp =
+        gptr(a.tt.table) + cu.g.seq_row * a.tt.stride + (pos >> a.tt.page_shift);
+    int page;
+    __asm__ volatile("global_load_dword %0, %1, off" : "=v"(page) : "v"(tp) : "memory");
+    return page;
+  };
+  // slot = page << page_shift | offset in page; applied after the load has landed
+  auto slot_of = [&](const Cursor& cu, int page) __attribute__((always_inline)) -> int {
+    const int key0 = cu.g.lo_min + cu.tile * kTile;
+    const int pos = min(key0 + (lane & 31), cu.g.seq - 1);
+    return (page << a.tt.page_shift) | (pos & ((1 << a.tt.page_shift) - 1));
+  };
+
+  // V rows go straight to LDS stage `stage` (global_load_lds, issued first), then K rows
+  // into registers. Loads complete in issue order, so once the compiler has waited for
+  // this tile's K registers, its V rows are in LDS as well.
+  auto issue = [&](const Cursor& cu, int myslot, Raw& r, int stage) __attribute__((always_inline)) {
+    const int64_t hoff = (int64_t)cu.h * head_bytes;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)vring[wave][stage];
+#pragma unroll
+    for (int x = 0; x < kVL; ++x) {
+      const int tok = kFp8 ? (8 * x + (lane >> 3)) : (4 * x + (lane >> 4));
+      const int pos = kFp8 ? (lane & 7) : (lane & 15);
+      const int slot = shfl_i(myslot, tok);
+      const unsigned char MA_GLOBAL* src = vbase + (int64_t)slot * row_bytes + hoff + ((pos ^ swz(tok)) << 4);
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + x * 1024);
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
+    }
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      const int slot = shfl_i(myslot, tb * 16 + c);
+      const unsigned char MA_GLOBAL* kp = kbase + (int64_t)slot * row_bytes + hoff;
+#pragma unroll
+      for (int x = 0; x < KR; ++x) {
+        const int off = kFp8 ? (j * DQ + x * 16) : (j * DQ + x * 8) * 2;
+        __asm__ volatile("global_load_dwordx4 %0, %1, off" : "=a"(r.k[tb][x]) : "v"(kp + off) : "memory");
+      }
+    }
+  };
+
+  // Wait until at most N of this wave's vector memory instructions are outstanding, then
+  // mark `regs` as produced here so that no use of them is scheduled above the wait.
+  auto wait_vm = [&](auto N_) __attribute__((always_inline)) {
+    constexpr int N = decltype(N_)::value;
+    __asm__ volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+  };
+  auto touch_k = [&](Raw& r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int x = 0; x < KR; ++x) __asm__ volatile("" : "+a"(r.k[tb][x]));
+  };
+
+  // ---- per-segment state ----
   int lo_r[NB], hi_r[NB];
   bool real[NB];
   u32x4 qv[NB][KK];
-  const uint16_t* qbase = reinterpret_cast<const uint16_t*>(a.q);
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int R = rg * kRows + nb * 16 + c;
-    const int t = R / a.group;
-    const int g = R - t * a.group;
-    real[nb] = t < si.ntok;
-    const int qpos = si.prefix + t;
-    int hi = a.causal ? min(si.seq, qpos + 1) : si.seq;
-    int lo = a.window >= 0 ? max(0, qpos - a.window) : 0;
-    lo_r[nb] = real[nb] ? max(lo, s0) : 0;
-    hi_r[nb] = real[nb] ? min(hi, s1) : 0;
-    const uint16_t* qp = qbase + (int64_t)(si.tok0 + t) * a.q_stride_tok +
-                         (int64_t)(h * a.group + g) * a.q_stride_head + j * DQ;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if (real[nb]) qv[nb][kk] = *reinterpret_cast<const u32x4*>(qp + kk * 8);
-      else qv[nb][kk] = u32x4{0, 0, 0, 0};
-    }
-  }
-  // Wave-uniform window in which every real row sees every key (no masking needed).
-  int lmax = -0x7fffffff, hmin = 0x7fffffff;
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    if (real[nb]) {
-      lmax = max(lmax, lo_r[nb]);
-      hmin = min(hmin, hi_r[nb]);
-    }
-  }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    lmax = max(lmax, __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, lmax));
-    hmin = min(hmin, __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, hmin));
-  }
-
-  // ---- online softmax state ----
   float m_run[NB], l_run[NB];
   f32x4 o[NB][DB];
+  int lmax = 0, hmin = 0;
+  bool first_piece = true;  // the current piece is the first piece of this wave's range
+  int piece_start_t = 0;    // wave-local tile where the current piece began
+
+  auto begin_segment = [&](const Cursor& cu) __attribute__((always_inline)) {
+    const uint16_t MA_GLOBAL* qbase = gptr(reinterpret_cast<const uint16_t*>(a.q));
+    const int s_end = cu.g.seq;
+    lmax = -0x7fffffff;
+    hmin = 0x7fffffff;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    m_run[nb] = -INFINITY;
-    l_run[nb] = 0.f;
+    for (int nb = 0; nb < NB; ++nb) {
+      const int R = cu.rg * kRows + nb * 16 + c;
+      const int t = R / a.group;
+      const int g = R - t * a.group;
+      real[nb] = t < cu.g.ntok;
+      const int qpos = cu.g.prefix + t;
+      const int hi = a.causal ? min(s_end, qpos + 1) : s_end;
+      const int lo = a.window >= 0 ? max(0, qpos - a.window) : 0;
+      lo_r[nb] = real[nb] ? lo : 0;
+      hi_r[nb] = real[nb] ? hi : 0;
+      if (real[nb]) {
+        lmax = max(lmax, lo);
+        hmin = min(hmin, hi);
+      }
+      const uint16_t MA_GLOBAL* qp = qbase + (int64_t)(cu.g.tok0 + t) * a.q_stride_tok +
+                                     (int64_t)(cu.h * a.group + g) * a.q_stride_head + j * DQ;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+      for (int kk = 0; kk < KK; ++kk)
+        qv[nb][kk] = real[nb] ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + kk * 8) : u32x4{0, 0, 0, 0};
+      m_run[nb] = -INFINITY;
+      l_run[nb] = 0.f;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      lmax = max(lmax, __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, lmax));
+      hmin = min(hmin, __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, hmin));
+    }
+  };
 
-  unsigned char* vt = smem + wave * D * kVtRow;
-  const unsigned char* kbase = reinterpret_cast<const unsigned char*>(a.k);
-  const unsigned char* vbase = reinterpret_cast<const unsigned char*>(a.v);
-  constexpr int kElt = kFp8 ? 1 : 2;
-  const int64_t row_bytes = a.kv_stride_row * kElt;
-  const int64_t head_off = (int64_t)h * a.kv_stride_head * kElt;
+  // Write this piece: the final output when it covers the whole segment, else a partial.
+  auto end_segment = [&](const Cursor& cu, bool whole, int slot_sel) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      float lt = l_run[nb];
+      lt += shfl_xor_f(lt, 16);
+      lt += shfl_xor_f(lt, 32);
+      if (!real[nb]) continue;
+      const int R = cu.rg * kRows + nb * 16 + c;
+      const int t = R / a.group;
+      const int g = R - t * a.group;
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      if (whole) {
+        uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) + (int64_t)(cu.g.tok0 + t) * a.out_stride_tok +
+                                 (int64_t)(cu.h * a.group + g) * a.out_stride_head;
+        const float sc = inv * a.v_scale;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          *reinterpret_cast<u32x2 MA_GLOBAL*>(op + db * 16 + 4 * j) = pack4<QBF16>(o[nb][db], sc);
+      } else {
+        const int64_t pidx = ((int64_t)W * 2 + slot_sel) * kMaxRows + nb * 16 + c;
+        float MA_GLOBAL* po = gptr_mut(a.part_o) + pidx * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4 MA_GLOBAL*>(po + db * 16 + 4 * j) = o[nb][db] * inv;
+        if (j == 0) {
+          const float mu = (m_run[nb] == -INFINITY) ? 0.f : m_run[nb];
+          gptr_mut(a.part_lse)[pidx] = lt > 0.f ? __builtin_amdgcn_logf(lt) + mu * a.scale_log2 : kEmptyLse;
+        }
+      }
+    }
+  };
 
-  for (int tb0 = s0 + kTile * wave; tb0 < s1; tb0 += kTile * kWaves) {
-    // slot of token (lane & 31) of the tile, spread to the lanes that load it
-    const int mypos = tb0 + (lane & 31);
-    int myslot = 0;
-    if (mypos < s1) myslot = (int)kv_row(a.tt, seq_row, mypos);
-
-    // ---- K: straight into the A-operand layout ----
+  auto compute = [&](const Cursor& cu, const Raw& r, int stage) __attribute__((always_inline)) {
+    const int tb0 = cu.g.lo_min + cu.tile * kTile;
+    const unsigned char* vt = vring[wave][stage];
+    // ---- K operand ----
     u32x4 kr[2][KK];
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
-      const int tok = tb * 16 + c;
-      const int slot = shfl_i(myslot, tok);
-      const bool ok = tb0 + tok < s1;
-      const unsigned char* kp = kbase + (int64_t)slot * row_bytes + head_off;
       if constexpr (kFp8) {
 #pragma unroll
-        for (int half = 0; half < KK / 2; ++half) {
-          u32x4 raw = ok ? *reinterpret_cast<const u32x4*>(kp + j * DQ + half * 16) : u32x4{0, 0, 0, 0};
-          cvt16_fp8<KV, QBF16>(raw, kr[tb][2 * half], kr[tb][2 * half + 1]);
-        }
+        for (int half = 0; half < KK / 2; ++half) cvt16_fp8<KV, QBF16>(r.k[tb][half], kr[tb][2 * half], kr[tb][2 * half + 1]);
       } else {
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
-          kr[tb][kk] = ok ? *reinterpret_cast<const u32x4*>(kp + (j * DQ + kk * 8) * 2) : u32x4{0, 0, 0, 0};
+        for (int kk = 0; kk < KK; ++kk) kr[tb][kk] = r.k[tb][kk];
       }
     }
-
-    // ---- V: load rows, convert to the PV operand type ----
-    // 16-bit: lane holds head-dim chunk (lane & 15) of tokens 4j+i and 16+4j+i.
-    // fp8:    lane holds head-dim chunk (lane & 7) (16 entries) of tokens 4(lane>>3)+i.
-    u32x4 vr[8];
-    if constexpr (kFp8) {
-      const int ch = lane & 7, qd = lane >> 3;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = 4 * qd + i;
-        const int slot = shfl_i(myslot, tok);
-        const bool ok = tb0 + tok < s1;
-        u32x4 raw = ok ? *reinterpret_cast<const u32x4*>(vbase + (int64_t)slot * row_bytes + head_off + ch * 16)
-                       : u32x4{0, 0, 0, 0};
-        cvt16_fp8<KV, false>(raw, vr[2 * i], vr[2 * i + 1]);
-      }
-    } else {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tok = 16 * hh + 4 * j + i;
-          const int slot = shfl_i(myslot, tok);
-          const bool ok = tb0 + tok < s1;
-          vr[4 * hh + i] = ok ? *reinterpret_cast<const u32x4*>(vbase + (int64_t)slot * row_bytes + head_off + c * 16)
-                              : u32x4{0, 0, 0, 0};
-        }
-      }
-    }
-
     // ---- S^T = K Q^T ----
     f32x4 s[NB][2];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -253,42 +422,7 @@ __global__ __launch_bounds__(256) void splitkv_partial(const SplitKVArgs a) {
         for (int kk = 0; kk < KK; ++kk) acc = mfma16t<QBF16>(kr[tb][kk], qv[nb][kk], acc);
         s[nb][tb] = acc;
       }
-    }
-
-    // ---- V^T tile into LDS (columns in the P^T token order) ----
-    if constexpr (kFp8) {
-      const int ch = lane & 7, qd = lane >> 3;
-      const int col = (qd < 4) ? 8 * qd : 8 * (qd - 4) + 4;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int w = e >> 1;  // dword inside the 16 converted values
-        uint32_t a0 = (w < 4) ? vr[0][w] : vr[1][w - 4];
-        uint32_t a1 = (w < 4) ? vr[2][w] : vr[3][w - 4];
-        uint32_t a2 = (w < 4) ? vr[4][w] : vr[5][w - 4];
-        uint32_t a3 = (w < 4) ? vr[6][w] : vr[7][w - 4];
-        u32x2 pk;
-        if (e & 1) { pk[0] = pack_hi(a0, a1); pk[1] = pack_hi(a2, a3); }
-        else { pk[0] = pack_lo(a0, a1); pk[1] = pack_lo(a2, a3); }
-        *reinterpret_cast<u32x2*>(vt + (ch * 16 + e) * kVtRow + col * 2) = pk;
-      }
-    } else {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int col = 8 * j + 4 * hh;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int w = e >> 1;
-          uint32_t a0 = vr[4 * hh + 0][w], a1 = vr[4 * hh + 1][w];
-          uint32_t a2 = vr[4 * hh + 2][w], a3 = vr[4 * hh + 3][w];
-          u32x2 pk;
-          if (e & 1) { pk[0] = pack_hi(a0, a1); pk[1] = pack_hi(a2, a3); }
-          else { pk[0] = pack_lo(a0, a1); pk[1] = pack_lo(a2, a3); }
-          *reinterpret_cast<u32x2*>(vt + (c * 8 + e) * kVtRow + col * 2) = pk;
-        }
-      }
-    }
-
-    // ---- online softmax (column = this lane's row) ----
+    // ---- online softmax ----
     const bool full = (tb0 >= lmax) && (tb0 + kTile <= hmin);
     u32x4 pb[NB], pl[NB];
     bool grew = false;
@@ -313,12 +447,13 @@ __global__ __launch_bounds__(256) void splitkv_partial(const SplitKVArgs a) {
       grew |= (m_new != m_run[nb]);
       alpha[nb] = __builtin_amdgcn_exp2f((m_run[nb] - m_use) * a.scale_log2);
       m_run[nb] = m_new;
+      const float msc = m_use * a.scale_log2;
       float p[8];
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[4 * tb + i] = __builtin_amdgcn_exp2f((s[nb][tb][i] - m_use) * a.scale_log2);
-      float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        for (int i = 0; i < 4; ++i) p[4 * tb + i] = __builtin_amdgcn_exp2f(s[nb][tb][i] * a.scale_log2 - msc);
+      const float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
       l_run[nb] = l_run[nb] * alpha[nb] + ps;
       if constexpr (kSplitP) {
 #pragma unroll
@@ -339,12 +474,30 @@ __global__ __launch_bounds__(256) void splitkv_partial(const SplitKVArgs a) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) o[nb][db] *= alpha[nb];
     }
-
     // ---- O^T += V^T P^T ----
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const u32x4 va = *reinterpret_cast<const u32x4*>(vt + (db * 16 + c) * kVtRow + j * 16);
+      u32x4 va;
+      if constexpr (kFp8) {
+        const int e = c >> 1, cc = lane & 1;
+        const int t = (e < 4) ? (4 * j + e) : (16 + 4 * j + e - 4);
+        const unsigned char* ptr = vt + t * kRowB + ((db ^ swz(t)) << 4) + cc * 8;
+        const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) i32x2*)(ptr)));
+        va = cvt8_fp8<KV, false>(raw[0], raw[1]);
+      } else {
+        const int e = c >> 2, cc = lane & 3;
+        const int chunk = 2 * db + (cc >> 1);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int t = 16 * half + 4 * j + e;
+          const unsigned char* ptr = vt + t * kRowB + ((chunk ^ swz(t)) << 4) + (cc & 1) * 8;
+          const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(ptr)));
+          va[2 * half] = raw[0];
+          va[2 * half + 1] = raw[1];
+        }
+      }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         o[nb][db] = mfma16t<kPvBf16>(va, pb[nb], o[nb][db]);
@@ -352,130 +505,163 @@ __global__ __launch_bounds__(256) void splitkv_partial(const SplitKVArgs a) {
       }
     }
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  }
+  };
 
-  // ---- merge the four waves ----
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    float lt = l_run[nb];
-    lt += shfl_xor_f(lt, 16);
-    lt += shfl_xor_f(lt, 32);
-    l_run[nb] = lt;
-    if (j == 0) {
-      sm_m[wave][nb * 16 + c] = m_run[nb];
-      sm_l[wave][nb * 16 + c] = lt;
+  // ---- cursors: slots run A tiles ahead of compute, K/V issue S-1 tiles ahead ----
+  // A = 2S-3 is the largest lead the S-entry slot ring allows, and it keeps the wait for a
+  // slot register from forcing any tile newer than the one about to be computed.
+  Cursor cc, ci, cs;
+  cursor_at(a, cc, b0, off0);
+  ci = cc;
+  cs = cc;
+  // Schedule. Step n: look up the slots of tile n+A, issue tile n+S-1 (its slots were
+  // looked up at step n+S-1-A), compute tile n (issued at step n-S+1). Steps -A..-1 form
+  // the prologue (no compute; tiles are issued from step 1-S on).
+  // Vector memory instructions issued at step k: one slot lookup, plus OPS-1 tile loads
+  // from step 1-S on. A wait for an instruction issued at step k0 keeps the instructions
+  // of later steps in flight.
+  auto ops_at = [](int k) constexpr -> int { return k >= 1 - S ? OPS : 1; };
+  auto ops_between = [ops_at](int k0, int k1) constexpr -> int {  // steps k0..k1 inclusive
+    int n = 0;
+    for (int k = k0; k <= k1; ++k) n += ops_at(k);
+    return n;
+  };
+  auto vstep = [&](auto N_) __attribute__((always_inline)) {
+    constexpr int N = decltype(N_)::value - A;
+    constexpr int SI = ((N + A) % S + S) % S;
+    sreg[SI] = load_slot(cs);
+    cursor_next(a, cs, count);
+    if constexpr (N + S - 1 >= 0) {
+      constexpr int RI = ((N + S - 1) % S + S) % S;
+      // the slot lookup of tile N+S-1 was issued at step N+S-1-A, first in its step
+      constexpr int W = ops_between(N + S - 1 - A, N - 1);
+      wait_vm(std::integral_constant<int, W>{});
+      __asm__ volatile("" : "+v"(sreg[RI]));
+      issue(ci, slot_of(ci, sreg[RI]), ring[RI], RI);
+      cursor_next(a, ci, count);
     }
-  }
-  __syncthreads();
-  float* acc = reinterpret_cast<float*>(smem);  // [kRows][D], reuses the V^T tiles
-  for (int idx = threadIdx.x; idx < kRows * D; idx += 256) acc[idx] = 0.f;
-  float M[NB], L[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int col = nb * 16 + c;
-    float mm = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sm_m[w][col]);
-    const float mu = (mm == -INFINITY) ? 0.f : mm;
-    float ll = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) ll += sm_l[w][col] * __builtin_amdgcn_exp2f((sm_m[w][col] - mu) * a.scale_log2);
-    M[nb] = mm;
-    L[nb] = ll;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const float mu = (M[nb] == -INFINITY) ? 0.f : M[nb];
-    const float f = (L[nb] > 0.f) ? __builtin_amdgcn_exp2f((m_run[nb] - mu) * a.scale_log2) / L[nb] : 0.f;
-    const int col = nb * 16 + c;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) atomicAdd(&acc[col * D + db * 16 + 4 * j + i], o[nb][db][i] * f);
-  }
-  __syncthreads();
+  };
+  [&]<int... Is>(std::integer_sequence<int, Is...>) __attribute__((always_inline)) {
+    (vstep(std::integral_constant<int, Is>{}), ...);
+  }(std::make_integer_sequence<int, A>{});
 
-  // ---- write: final output when this sequence has one split, else a partial ----
-  const bool direct = (si.active == 1);
-  for (int idx = threadIdx.x; idx < kRows * (D / 4); idx += 256) {
-    const int col = idx / (D / 4);
-    const int d4 = (idx - col * (D / 4)) * 4;
-    const int R = rg * kRows + col;
-    const int t = R / a.group;
-    const int g = R - t * a.group;
-    if (t >= si.ntok) continue;
-    const int tok = si.tok0 + t;
-    const int head = h * a.group + g;
-    f32x4 val = *reinterpret_cast<const f32x4*>(&acc[col * D + d4]);
-    if (direct) {
-      const int64_t off = (int64_t)tok * a.out_stride_tok + (int64_t)head * a.out_stride_head + d4;
-      uint16_t* op = reinterpret_cast<uint16_t*>(a.out) + off;
-      u32x2 pk;
-      pk[0] = (uint32_t)f2h<QBF16>(val[0] * a.v_scale) | ((uint32_t)f2h<QBF16>(val[1] * a.v_scale) << 16);
-      pk[1] = (uint32_t)f2h<QBF16>(val[2] * a.v_scale) | ((uint32_t)f2h<QBF16>(val[3] * a.v_scale) << 16);
-      *reinterpret_cast<u32x2*>(op) = pk;
-    } else {
-      const int64_t qrow = (int64_t)tok * a.hq + head;
-      *reinterpret_cast<f32x4*>(a.part_o + ((int64_t)split * a.qrows + qrow) * D + d4) = val;
+  auto step = [&](auto I_, int n) __attribute__((always_inline)) {
+    constexpr int I = decltype(I_)::value;
+    constexpr int RI = (I + S - 1) % S;
+    // slot of tile n+A -> sreg[(n+A) % S] (that register's previous tile is already issued)
+    sreg[(I + A) % S] = load_slot(cs);
+    cursor_next(a, cs, count);
+    // K/V of tile n+S-1, once its slot lookup (A-S+1 steps ago) has landed
+    wait_vm(std::integral_constant<int, OPS * (A - S + 1)>{});
+    __asm__ volatile("" : "+v"(sreg[RI]));
+    issue(ci, slot_of(ci, sreg[RI]), ring[RI], RI);
+    cursor_next(a, ci, count);
+    if (n < count) {
+      if (cc.t == 0 || cc.tile == 0) {
+        begin_segment(cc);
+        piece_start_t = cc.t;
+      }
+      // tile n was issued at step n-S+1; the S-1 steps since then keep their loads in flight
+      wait_vm(std::integral_constant<int, (S - 1) * OPS>{});
+      touch_k(ring[I]);
+      compute(cc, ring[I], I);
+      const bool seg_last = (cc.tile == cc.g.nt - 1);
+      const bool range_last = (n == count - 1);
+      if (seg_last || range_last) {
+        const bool whole = seg_last && (cc.tile == cc.t - piece_start_t);
+        // slot 0: the first piece of the range (also a single-piece range); slot 1: the last
+        end_segment(cc, whole, first_piece ? 0 : 1);
+        first_piece = false;
+      }
+      cursor_next(a, cc, count);
     }
-  }
-  if (!direct && threadIdx.x < kRows) {
-    const int col = threadIdx.x;
-    const int R = rg * kRows + col;
-    const int t = R / a.group;
-    const int g = R - t * a.group;
-    if (t < si.ntok) {
-      const int nbk = col >> 4;
-      float mm = -INFINITY, ll = 0.f;
-      // M/L for this column live in the lanes of wave 0 with c == col & 15
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sm_m[w][col]);
-      const float mu = (mm == -INFINITY) ? 0.f : mm;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) ll += sm_l[w][col] * __builtin_amdgcn_exp2f((sm_m[w][col] - mu) * a.scale_log2);
-      (void)nbk;
-      const int64_t qrow = (int64_t)(si.tok0 + t) * a.hq + h * a.group + g;
-      a.part_lse[(int64_t)split * a.qrows + qrow] = (ll > 0.f) ? __builtin_amdgcn_logf(ll) + mu * a.scale_log2 : kEmptyLse;
-    }
-  }
+  };
+
+  auto group = [&]<int... Is>(std::integer_sequence<int, Is...>, int n) __attribute__((always_inline)) {
+    (step(std::integral_constant<int, Is>{}, n + Is), ...);
+  };
+  for (int n = 0; n < count; n += S) group(std::make_integer_sequence<int, S>{}, n);
 }
 
 // ---------------------------------------------------------------------------
-// Combine: LSE-weighted merge of the split partials (log2 domain).
-// grid (ceil(hq / 8), max_tokens_per_seq, batch), 256 threads: 32 threads per head,
-// 4 head-dim entries per thread.
+// Combine: one workgroup per segment (sequence, kv head, row group). Merges the
+// partial pieces of a segment that several waves shared, writes zeros for a segment
+// with real rows but no keys, and leaves whole segments (already written) alone.
 // ---------------------------------------------------------------------------
 template <int D, bool QBF16>
 __global__ __launch_bounds__(256) void splitkv_combine(const SplitKVArgs a) {
-  constexpr int TPH = D / 4;           // threads per head
-  constexpr int HPB = 256 / TPH;       // heads per block
-  const int b = blockIdx.z;
-  const int t = blockIdx.y;
-  const SeqInfo si = seq_info(a, b);
-  if (si.active == 1 || t >= si.ntok) return;
-  const int head = blockIdx.x * HPB + threadIdx.x / TPH;
-  if (head >= a.hq) return;
-  const int d4 = (threadIdx.x % TPH) * 4;
-  const int tok = si.tok0 + t;
-  const int64_t qrow = (int64_t)tok * a.hq + head;
-  float mx = -INFINITY;
-  for (int s = 0; s < si.active; ++s) mx = fmaxf(mx, a.part_lse[(int64_t)s * a.qrows + qrow]);
-  float wsum = 0.f;
-  f32x4 accv = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < si.active; ++s) {
-    const float w = __builtin_amdgcn_exp2f(a.part_lse[(int64_t)s * a.qrows + qrow] - mx);
-    wsum += w;
-    const f32x4 po = *reinterpret_cast<const f32x4*>(a.part_o + ((int64_t)s * a.qrows + qrow) * D + d4);
-    accv += po * w;
+  const int seg = blockIdx.x;
+  const int rg = seg % a.row_groups;
+  const int h = (seg / a.row_groups) % a.hkv;
+  const int b = seg / (a.row_groups * a.hkv);
+  const Geom g = geom(a, b);
+  if (rg >= g.rg_real) return;
+  __shared__ int64_t s_red[2][256];
+  int64_t before = 0, all = 0;
+  for (int x = threadIdx.x; x < a.batch; x += 256) {
+    const int w = seq_work(a, x);
+    all += w;
+    if (x < b) before += w;
   }
-  const float inv = a.v_scale / wsum;
-  const int64_t off = (int64_t)tok * a.out_stride_tok + (int64_t)head * a.out_stride_head + d4;
-  uint16_t* op = reinterpret_cast<uint16_t*>(a.out) + off;
-  u32x2 pk;
-  pk[0] = (uint32_t)f2h<QBF16>(accv[0] * inv) | ((uint32_t)f2h<QBF16>(accv[1] * inv) << 16);
-  pk[1] = (uint32_t)f2h<QBF16>(accv[2] * inv) | ((uint32_t)f2h<QBF16>(accv[3] * inv) << 16);
-  *reinterpret_cast<u32x2*>(op) = pk;
+  s_red[0][threadIdx.x] = before;
+  s_red[1][threadIdx.x] = all;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (threadIdx.x < st) {
+      s_red[0][threadIdx.x] += s_red[0][threadIdx.x + st];
+      s_red[1][threadIdx.x] += s_red[1][threadIdx.x + st];
+    }
+    __syncthreads();
+  }
+  before = s_red[0][0];
+  const int64_t total = s_red[1][0];
+  const int rows = a.rows;
+  if (g.nt == 0) {
+    // real rows that see no key: zero output
+    for (int idx = threadIdx.x; idx < rows * D; idx += 256) {
+      const int col = idx / D, d = idx - col * D;
+      const int R = rg * rows + col;
+      const int t = R / a.group, gg = R - t * a.group;
+      if (t >= g.ntok) continue;
+      reinterpret_cast<uint16_t*>(a.out)[(int64_t)(g.tok0 + t) * a.out_stride_tok +
+                                         (int64_t)(h * a.group + gg) * a.out_stride_head + d] = 0;
+    }
+    return;
+  }
+  const int64_t first = before + (int64_t)(h * g.rg_real + rg) * g.nt;
+  const int64_t last = first + g.nt - 1;
+  const int w1 = wave_of(first, total, a.nwaves);
+  const int w2 = wave_of(last, total, a.nwaves);
+  if (w1 == w2) return;  // one wave covered the segment and wrote the output
+  const bool w1_second = first > wave_begin(w1, total, a.nwaves);
+  // 32 threads per row, 4 head-dim entries each; 8 rows per pass
+  for (int base = 0; base < rows; base += 8) {
+    const int col = base + threadIdx.x / 32;
+    const int d4 = (threadIdx.x % 32) * 4;
+    const int R = rg * rows + col;
+    const int t = R / a.group, gg = R - t * a.group;
+    if (col >= rows || t >= g.ntok) continue;
+    // waves with an empty range (more waves than tiles) hold no piece
+    float mx = -INFINITY;
+    for (int w = w1; w <= w2; ++w) {
+      if (wave_begin(w + 1, total, a.nwaves) == wave_begin(w, total, a.nwaves)) continue;
+      const int sel = (w == w1 && w1_second) ? 1 : 0;
+      mx = fmaxf(mx, a.part_lse[((int64_t)w * 2 + sel) * kMaxRows + col]);
+    }
+    float wsum = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int w = w1; w <= w2; ++w) {
+      if (wave_begin(w + 1, total, a.nwaves) == wave_begin(w, total, a.nwaves)) continue;
+      const int sel = (w == w1 && w1_second) ? 1 : 0;
+      const int64_t pidx = ((int64_t)w * 2 + sel) * kMaxRows + col;
+      const float wt = __builtin_amdgcn_exp2f(a.part_lse[pidx] - mx);
+      wsum += wt;
+      acc += *reinterpret_cast<const f32x4*>(a.part_o + pidx * D + d4) * wt;
+    }
+    uint16_t* op = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(g.tok0 + t) * a.out_stride_tok +
+                   (int64_t)(h * a.group + gg) * a.out_stride_head + d4;
+    *reinterpret_cast<u32x2*>(op) = pack4<QBF16>(acc, a.v_scale / wsum);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -494,30 +680,34 @@ static hipError_t launch_partial_kv(int kv, dim3 grid, hipStream_t st, const Spl
 
 template <int D>
 static hipError_t launch_partial_d(int nb, bool qbf16, int kv, dim3 grid, hipStream_t st, const SplitKVArgs& a) {
-  if (qbf16) {
-    if (nb == 1) return launch_partial_kv<D, 1, true>(kv, grid, st, a);
-    if (nb == 2) return launch_partial_kv<D, 2, true>(kv, grid, st, a);
-    return launch_partial_kv<D, 4, true>(kv, grid, st, a);
-  }
-  if (nb == 1) return launch_partial_kv<D, 1, false>(kv, grid, st, a);
-  if (nb == 2) return launch_partial_kv<D, 2, false>(kv, grid, st, a);
-  return launch_partial_kv<D, 4, false>(kv, grid, st, a);
-}
-
-template <int D>
-static hipError_t launch_combine_d(bool qbf16, dim3 grid, hipStream_t st, const SplitKVArgs& a) {
-  if (qbf16) hipLaunchKernelGGL((splitkv_combine<D, true>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((splitkv_combine<D, false>), grid, dim3(256), 0, st, a);
-  return hipGetLastError();
+  if (qbf16) return nb == 1 ? launch_partial_kv<D, 1, true>(kv, grid, st, a) : launch_partial_kv<D, 2, true>(kv, grid, st, a);
+  return nb == 1 ? launch_partial_kv<D, 1, false>(kv, grid, st, a) : launch_partial_kv<D, 2, false>(kv, grid, st, a);
 }
 
 }  // namespace ma
 
 using namespace ma;
 
-// Common body of ma_grouped_decode and ma_paged_verify.
+static int device_workgroups(int requested) {
+  if (requested > 0) return requested;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+  return cus;
+}
+
+extern "C" size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim) {
+  if (num_workgroups <= 0 || head_dim <= 0) return 0;
+  const size_t pieces = (size_t)num_workgroups * kWaves * 2 * kMaxRows;
+  size_t o = pieces * head_dim * sizeof(float);
+  o = (o + 255) & ~(size_t)255;
+  return o + ((pieces * sizeof(float) + 255) & ~(size_t)255);
+}
+
+extern "C" int ma_device_workgroups(void) { return device_workgroups(0); }
+
 static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, int max_q_per_seq,
-                       size_t workspace_bytes, hipStream_t stream) {
+                       int num_workgroups, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (head_dim != 128) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (128)", head_dim);
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
   if (kv_dtype < 0 || kv_dtype > DT_E5M2) return set_error(MA_EINVAL, "kv dtype %d unknown", kv_dtype);
@@ -525,10 +715,10 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
     return set_error(MA_EINVAL, "16-bit KV dtype must equal the query dtype");
   if (a.batch < 0 || a.hq <= 0 || a.hkv <= 0 || a.hq % a.hkv)
     return set_error(MA_EINVAL, "bad head counts hq=%d hkv=%d", a.hq, a.hkv);
-  if (a.max_splits <= 0 || a.min_tokens <= 0) return set_error(MA_EINVAL, "max_splits and min_tokens must be positive");
   if (!(a.scale_log2 > 0.f)) return set_error(MA_EINVAL, "softmax scale must be positive");
   if (a.tt.page_shift < 0 || a.tt.page_shift > 16) return set_error(MA_EINVAL, "bad page shift");
   if (max_q_per_seq <= 0) return set_error(MA_EINVAL, "max query rows per sequence must be positive");
+  if (num_workgroups <= 0) return set_error(MA_EINVAL, "num_workgroups must be positive (ma_device_workgroups())");
   if (a.batch == 0) return MA_OK;
   if (!a.q || !a.k || !a.v || !a.tt.table || !a.seq_lens || !a.out)
     return set_error(MA_EINVAL, "null pointer argument");
@@ -540,43 +730,27 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
       ((a.q_stride_head * 2) & 15) || ((a.out_stride_tok * 2) & 7) || ((a.out_stride_head * 2) & 7))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   a.group = a.hq / a.hkv;
-  const int rows = max_q_per_seq * a.group;
-  const int nb = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
-  a.row_groups = (rows + 16 * nb - 1) / (16 * nb);
-  const size_t need = ma_splitkv_workspace_bytes(a.max_splits, a.qrows / a.hq, a.hq, head_dim);
-  if (a.max_splits > 1 && (!a.part_o || workspace_bytes < need))
+  const int rows_total = max_q_per_seq * a.group;
+  const int nb = rows_total <= 16 ? 1 : 2;
+  a.rows = 16 * nb;
+  a.row_groups = (rows_total + a.rows - 1) / a.rows;
+  a.nwaves = num_workgroups * kWaves;
+  const size_t need = ma_splitkv_workspace_bytes(num_workgroups, head_dim);
+  if (!workspace || workspace_bytes < need)
     return set_error(MA_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
-  dim3 grid(a.hkv * a.row_groups, a.max_splits, a.batch);
-  hipError_t e = launch_partial_d<128>(nb, q_dtype == DT_BF16, kv_dtype, grid, stream, a);
+  const size_t pieces = (size_t)num_workgroups * kWaves * 2 * kMaxRows;
+  const size_t o_bytes = (pieces * head_dim * sizeof(float) + 255) & ~(size_t)255;
+  a.part_o = reinterpret_cast<float*>(workspace);
+  a.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + o_bytes);
+  const int64_t segs = (int64_t)a.batch * a.hkv * a.row_groups;
+  if (segs > 0x7fffffff) return set_error(MA_EINVAL, "too many segments");
+  hipError_t e = launch_partial_d<128>(nb, q_dtype == DT_BF16, kv_dtype, dim3(num_workgroups), stream, a);
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "partial launch failed: %s", hipGetErrorString(e));
-  if (a.max_splits > 1) {
-    dim3 cg((a.hq + 7) / 8, max_q_per_seq, a.batch);
-    e = launch_combine_d<128>(q_dtype == DT_BF16, cg, stream, a);
-    if (e != hipSuccess) return set_error(MA_ELAUNCH, "combine launch failed: %s", hipGetErrorString(e));
-  }
+  if (q_dtype == DT_BF16) hipLaunchKernelGGL((splitkv_combine<128, true>), dim3((unsigned)segs), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((splitkv_combine<128, false>), dim3((unsigned)segs), dim3(256), 0, stream, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return set_error(MA_ELAUNCH, "combine launch failed: %s", hipGetErrorString(e));
   return MA_OK;
-}
-
-extern "C" size_t ma_splitkv_workspace_bytes(int max_splits, int64_t num_tokens, int num_q_heads, int head_dim) {
-  if (max_splits <= 1) return 0;
-  const int64_t rows = num_tokens * (int64_t)num_q_heads;
-  // partial O then partial LSE, each 256-byte aligned
-  size_t o = (size_t)max_splits * rows * head_dim * sizeof(float);
-  o = (o + 255) & ~(size_t)255;
-  size_t l = (size_t)max_splits * rows * sizeof(float);
-  return o + ((l + 255) & ~(size_t)255);
-}
-
-static void split_workspace(SplitKVArgs& a, void* ws, int64_t rows, int head_dim) {
-  if (!ws || a.max_splits <= 1) {
-    a.part_o = nullptr;
-    a.part_lse = nullptr;
-    return;
-  }
-  size_t o = (size_t)a.max_splits * rows * head_dim * sizeof(float);
-  o = (o + 255) & ~(size_t)255;
-  a.part_o = reinterpret_cast<float*>(ws);
-  a.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + o);
 }
 
 extern "C" int ma_grouped_decode(
@@ -584,7 +758,7 @@ extern "C" int ma_grouped_decode(
     const void* k_cache, const void* v_cache, int64_t kv_stride_row, int64_t kv_stride_head, int kv_dtype,
     const int32_t* table, int64_t table_stride, const int64_t* row_index, int page_size,
     const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
-    int max_splits, int min_tokens_per_split, float softmax_scale, float k_scale, float v_scale,
+    int num_workgroups, float softmax_scale, float k_scale, float v_scale,
     int sliding_window, void* workspace, size_t workspace_bytes,
     void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
@@ -594,13 +768,11 @@ extern "C" int ma_grouped_decode(
   a.tt.table = table; a.tt.stride = table_stride; a.tt.page_shift = __builtin_ctz(page_size);
   a.row_index = row_index; a.seq_lens = seq_lens; a.qsl = nullptr; a.prefix = nullptr;
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads;
-  a.max_splits = max_splits; a.min_tokens = min_tokens_per_split;
   a.causal = 1; a.window = sliding_window < 0 ? -1 : sliding_window;
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
-  a.qrows = (int64_t)batch * num_q_heads;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
-  split_workspace(a, workspace, a.qrows, head_dim);
-  return splitkv_run(a, head_dim, q_dtype, kv_dtype, 1, workspace_bytes, (hipStream_t)stream);
+  return splitkv_run(a, head_dim, q_dtype, kv_dtype, 1, num_workgroups, workspace, workspace_bytes,
+                     (hipStream_t)stream);
 }
 
 extern "C" int ma_paged_verify(
@@ -609,9 +781,10 @@ extern "C" int ma_paged_verify(
     const int32_t* table, int64_t table_stride, const int64_t* row_index, int page_size,
     const int32_t* seq_lens, const int32_t* query_start_loc, const int32_t* prefix_lens,
     int batch, int max_q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
-    int causal, int sliding_window, int max_splits, int min_tokens_per_split,
+    int causal, int sliding_window, int num_workgroups,
     float softmax_scale, float k_scale, float v_scale, void* workspace, size_t workspace_bytes,
     void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+  (void)num_tokens;
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
   if (!query_start_loc) return set_error(MA_EINVAL, "query_start_loc is required");
   if (max_q_per_seq > 64) return set_error(MA_EUNSUPPORTED, "verify supports at most 64 query rows per sequence");
@@ -621,11 +794,9 @@ extern "C" int ma_paged_verify(
   a.tt.table = table; a.tt.stride = table_stride; a.tt.page_shift = __builtin_ctz(page_size);
   a.row_index = row_index; a.seq_lens = seq_lens; a.qsl = query_start_loc; a.prefix = prefix_lens;
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads;
-  a.max_splits = max_splits; a.min_tokens = min_tokens_per_split;
   a.causal = causal ? 1 : 0; a.window = sliding_window < 0 ? -1 : sliding_window;
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
-  a.qrows = num_tokens * num_q_heads;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
-  split_workspace(a, workspace, a.qrows, head_dim);
-  return splitkv_run(a, head_dim, q_dtype, kv_dtype, max_q_per_seq, workspace_bytes, (hipStream_t)stream);
+  return splitkv_run(a, head_dim, q_dtype, kv_dtype, max_q_per_seq, num_workgroups, workspace, workspace_bytes,
+                     (hipStream_t)stream);
 }

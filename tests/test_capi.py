@@ -54,7 +54,7 @@ def test_abi_version(lib):
 def _decode_args(**over):
     args = dict(q=1 << 20, qs0=1024, qs1=128, qdt=1, k=1 << 21, v=1 << 22, rs=1024, hs=128, kvdt=1,
                 table=1 << 23, tstride=64, rowidx=None, ps=1, seq=1 << 24, batch=2, hq=8, hkv=8, dim=128,
-                splits=1, mintok=256, sm=0.1, ks=1.0, vs=1.0, win=-1, ws=None, wsb=0,
+                nwg=4, sm=0.1, ks=1.0, vs=1.0, win=-1, ws=None, wsb=0,
                 out=1 << 25, os0=1024, os1=128, stream=None)
     args.update(over)
     return list(args.values())
@@ -68,7 +68,9 @@ def _decode_args(**over):
     ({"ps": 3}, "power of two"),
     ({"sm": 0.0}, "scale"),
     ({"q": (1 << 20) + 2}, "aligned"),
-    ({"splits": 4, "ws": None, "wsb": 0}, "workspace"),
+    ({"ws": None, "wsb": 0}, "workspace"),
+    ({"ws": 1 << 26, "wsb": 1024}, "workspace too small"),
+    ({"nwg": 0}, "num_workgroups"),
 ])
 def test_bad_arguments_are_rejected_before_launch(lib, over, msg):
     status = lib.ma_grouped_decode(*_decode_args(**over))
@@ -81,6 +83,7 @@ def test_empty_batch_is_a_no_op(lib):
 
 
 def test_workspace_size_formula(lib):
-    assert lib.ma_splitkv_workspace_bytes(1, 64, 64, 128) == 0
-    n = lib.ma_splitkv_workspace_bytes(4, 64, 64, 128)
-    assert n >= 4 * 64 * 64 * 129 * 4 and n % 256 == 0
+    assert lib.ma_splitkv_workspace_bytes(0, 128) == 0
+    n = lib.ma_splitkv_workspace_bytes(256, 128)
+    # two partial pieces of up to 32 rows per wave, 4 waves per workgroup
+    assert n >= 256 * 4 * 2 * 32 * 129 * 4 and n % 256 == 0
