@@ -12,10 +12,22 @@ resident in HBM:
 * ``--secondary`` adds the other workloads (extend TFLOP/s, fp8 decode GB/s,
   verify GB/s) as extra fields of the same JSON line.
 
-``roofline`` compares the dominant launch's algorithmic bytes / HIP-event time
-with the 8 TB/s HBM peak. ``cpu_baseline`` times the torch-native SDPA
-restatement of the same workload (per-sequence gather + fp32 SDPA) on this
-host's cores. Prints exactly one JSON line.
+``value`` is whole-job throughput: algorithmic bytes of the K timed steps over
+the wall time between the two synchronisations. ``roofline`` compares the
+algorithmic bytes of one call with its HIP-event duration on the launch stream
+against the 8 TB/s HBM peak; ``roofline.traffic`` is the measured HBM bytes per
+launch of the dominant kernel, read from the committed counter summary
+(profiles/<kernel>__<workload>.traffic.md) when one exists for this workload.
+``cpu_baseline`` times the torch-native SDPA restatement of the same workload
+(per-sequence gather + fp32 SDPA) on this host's cores. Prints exactly one
+JSON line.
+
+    python bench.py --calibrate-copy 1024
+
+copies a 1024 MiB float32 buffer five times with a plain elementwise kernel
+(torch.neg into a second buffer: 1 GiB read, 1 GiB written per launch): the
+FETCH_SIZE / WRITE_SIZE counters of those launches scale the counters of the
+attention kernels to bytes.
 """
 
 from __future__ import annotations
@@ -41,7 +53,36 @@ def _parse():
     p.add_argument("--secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0)
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     return p.parse_args()
+
+
+def _calibrate_copy(mib):
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / 5
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5,
+                      "GBps_read_plus_write": 2 * n / dt / 1e9}))
+
+
+def _traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from its committed counter summary."""
+    import re
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"{kernel}__{workload}.traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
 
 
 def _runner(w):
@@ -141,7 +182,7 @@ def _cpu_baseline(w, budget_s):
 
 
 def _workload_metrics(w):
-    from oracle import workloads
+    from sglang_restomod_amd import workloads
 
     return workloads.algorithmic_bytes(w), workloads.algorithmic_flops(w)
 
@@ -149,7 +190,7 @@ def _workload_metrics(w):
 def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
     import torch
 
-    from oracle import workloads
+    from sglang_restomod_amd import workloads
 
     w = workloads.make(index, device=torch.device("cuda:0"), kv_format=kv_format)
     fn = _runner(w)
@@ -167,6 +208,8 @@ def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
         "algorithmic_flops": flops,
         "GBps": nbytes / (ev_ms * 1e-3) / 1e9,
         "TFLOPs": flops / (ev_ms * 1e-3) / 1e12,
+        "wall_GBps": nbytes / (wall_ms * 1e-3) / 1e9,
+        "wall_TFLOPs": flops / (wall_ms * 1e-3) / 1e12,
         "tokens_per_s": (w.batch if w.mode == "decode" else int(w.extend_lens.sum())) / (wall_ms * 1e-3),
     }
     res["hbm_frac"] = res["GBps"] / HBM_PEAK_GBS
@@ -187,8 +230,8 @@ def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
 def main():
     args = _parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(sharding across GPUs is described in DESIGN.md, not launched)"}))
+        print(json.dumps({"error": "the attention path is measured on one GPU only; --gpus must be 1 "
+                                   "(how it shards across GPUs is documented, not launched)"}))
         sys.exit(2)
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import torch
@@ -196,11 +239,15 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if args.calibrate_copy:
+        _calibrate_copy(args.calibrate_copy)
+        return
     head = _measure(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_seconds)
     bound_hbm = head["mode"] != "extend"
+    kernel = "splitkv_partial" if bound_hbm else "extend_kernel"
     line = {
         "metric": METRIC,
-        "value": round(head["GBps"] if bound_hbm else head["TFLOPs"], 3),
+        "value": round(head["wall_GBps"] if bound_hbm else head["wall_TFLOPs"], 3),
         "unit": "GB/s" if bound_hbm else "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -219,9 +266,10 @@ def main():
             "peak": HBM_PEAK_GBS if bound_hbm else MFMA_BF16_PEAK_TFLOPS,
             "unit": "GB/s" if bound_hbm else "TFLOP/s",
             "frac": round(head["hbm_frac"] if bound_hbm else head["mfma_frac"], 4),
-            "traffic": None,
+            "traffic": _traffic(kernel, head["workload"]),
             "kernel_ms": round(head["event_ms_mean"], 5),
-            "timing": "HIP events on the launch stream around each call (split-KV partial + combine)",
+            "timing": ("HIP events on the launch stream around each call (split-KV partial + combine)"
+                       if bound_hbm else "HIP events on the launch stream around each call"),
         },
     }
     if "cpu" in head:

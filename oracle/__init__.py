@@ -17,7 +17,9 @@ Modules
                   CPU baseline.
 ``fp8``           bit-level decoding of OCP e4m3fn / e5m2 bytes.
 ``metadata``      page-table / query-start / verify-row metadata construction.
-``workloads``     seeded generators for the five benchmark configurations.
+
+The seeded generators of the five benchmark workloads are not part of the oracle:
+they live in ``sglang_restomod_amd/workloads.py``.
 
 How each function is pinned (so that a plausible mistake fails a test) is
 listed in its docstring and exercised in ``tests/test_oracle_*.py``.

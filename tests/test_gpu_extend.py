@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import attention as oracle
-from oracle import workloads
+from sglang_restomod_amd import workloads
 from tests.helpers import assert_attn_close, to_f64
 
 pytestmark = pytest.mark.gpu
@@ -47,7 +47,7 @@ def _check_rows(q, k_pool, v_pool, slots_of, prefix, qsl, out, rows_of, scale, k
 def _workload_extend(gpu, batch=None, scale_lens=1.0, sample=None, kv_format=None):
     w = workloads.make(2, device=gpu, batch=batch, scale_lens=scale_lens)
     if kv_format is not None:
-        from oracle.workloads import FP8
+        from sglang_restomod_amd.workloads import FP8
 
         w.k_scale, w.v_scale = 0.75, 1.5
         w.k_pool = (w.k_pool.float() / w.k_scale).to(FP8[kv_format])

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import attention as oracle
-from oracle import workloads
+from sglang_restomod_amd import workloads
 from tests.helpers import assert_attn_close, to_f64
 
 pytestmark = pytest.mark.gpu

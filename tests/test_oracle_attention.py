@@ -14,7 +14,7 @@ import torch.nn.functional as F
 
 from oracle import attention as A
 from oracle import torch_native as TN
-from oracle import workloads
+from sglang_restomod_amd import workloads
 
 
 def _rand(*shape, seed=0):
