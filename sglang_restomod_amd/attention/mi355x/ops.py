@@ -23,6 +23,7 @@ from . import _lib
 FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 
 VERIFY_MAX_Q_PER_SEQ = 64
+SUPPORTED_HEAD_DIMS = (128,)
 
 _WORKSPACES: dict = {}
 _DEVICE_WORKGROUPS: dict = {}
@@ -125,6 +126,24 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+def splitkv_workspace(device: torch.device, num_workgroups: Optional[int] = None,
+                      head_dim: int = 128) -> torch.Tensor:
+    """A fresh workspace sized for the split-KV entry points at this grid (callers that
+    capture graphs keep one for the graph's lifetime instead of the shared buffer)."""
+    nwg = int(num_workgroups) if num_workgroups else splitkv_workgroups(device)
+    nbytes = _lib.load().ma_splitkv_workspace_bytes(nwg, head_dim)
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+
+
+def _splitkv_ws(lib, dev, nwg: int, D: int, given: Optional[torch.Tensor]):
+    nbytes = lib.ma_splitkv_workspace_bytes(nwg, D)
+    if given is None:
+        return workspace(dev, nbytes), nbytes
+    if given.dtype != torch.uint8 or given.device != dev or given.numel() < nbytes:
+        raise ValueError(f"workspace must be a uint8 tensor of at least {nbytes} bytes on {dev}")
+    return given, nbytes
+
+
 def _i32(t: torch.Tensor) -> torch.Tensor:
     return t if (t.dtype == torch.int32 and t.is_contiguous()) else t.to(torch.int32).contiguous()
 
@@ -157,12 +176,15 @@ def grouped_decode_forward(
     sliding_window_size: int = -1,
     max_seq_len_hint: Optional[int] = None,
     num_workgroups: Optional[int] = None,
+    workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Decode one query token per sequence: ``q`` [B, Hq, D] -> [B, Hq, D] (q's dtype).
 
     ``page_table`` [rows, width] int32 maps (row, position // page_size) to a page;
     ``row_index`` [B] picks each sequence's row (None: row b). With page size 1
     and ``req_to_token`` / ``req_pool_indices`` this reads SGLang's slots directly.
+    ``workspace``: a uint8 buffer from ``splitkv_workspace`` (None: a shared buffer
+    per device and stream).
     """
     if q.dim() != 3:
         raise ValueError(f"q must be [batch, heads, head_dim], got {tuple(q.shape)}")
@@ -190,8 +212,7 @@ def grouped_decode_forward(
     del max_seq_len_hint  # the persistent grid does not depend on lengths
     nwg = int(num_workgroups) if num_workgroups else splitkv_workgroups(dev)
     lib = _lib.load()
-    nbytes = lib.ma_splitkv_workspace_bytes(nwg, D)
-    ws = workspace(dev, nbytes)
+    ws, nbytes = _splitkv_ws(lib, dev, nwg, D, workspace)
     status = lib.ma_grouped_decode(
         q.data_ptr(), q.stride(0), q.stride(1), q_dtype_code(q.dtype),
         k_cache.data_ptr(), v_cache.data_ptr(), row, head, kv_dtype_code(k_cache.dtype),
@@ -225,6 +246,7 @@ def paged_verify_forward(
     page_size: Optional[int] = None,
     max_seq_len_hint: Optional[int] = None,
     num_workgroups: Optional[int] = None,
+    workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Few query rows per sequence over a long prefix (linear-chain target verify)."""
     if q.dim() != 3:
@@ -251,8 +273,7 @@ def paged_verify_forward(
     del max_seq_len_hint
     nwg = int(num_workgroups) if num_workgroups else splitkv_workgroups(dev)
     lib = _lib.load()
-    nbytes = lib.ma_splitkv_workspace_bytes(nwg, D)
-    ws = workspace(dev, nbytes)
+    ws, nbytes = _splitkv_ws(lib, dev, nwg, D, workspace)
     status = lib.ma_paged_verify(
         q.data_ptr(), q.stride(0), q.stride(1), q_dtype_code(q.dtype), T,
         k_cache.data_ptr(), v_cache.data_ptr(), row, head, kv_dtype_code(k_cache.dtype),
@@ -288,6 +309,7 @@ def paged_forward(
     logical_dense_kv: bool = False,
     row_index: Optional[torch.Tensor] = None,
     max_q_len_hint: Optional[int] = None,
+    workspace: Optional[torch.Tensor] = None,
 ):
     """Prefix-aware paged attention over ``q`` [num_tokens, Hq, D] (reference: paged_forward).
 
@@ -312,7 +334,7 @@ def paged_forward(
             q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
             max_q_per_seq=max_q_len_hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
             causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
-            page_size=block_size, max_seq_len_hint=max_seq_len_hint)
+            page_size=block_size, max_seq_len_hint=max_seq_len_hint, workspace=workspace)
     return paged_extend_forward(
         q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
         max_q_len=max_q_len_hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,

@@ -1,0 +1,175 @@
+"""End-to-end through MI355XAttnBackend on the GPU: a serving sequence over the
+fake engine (cached prefix -> extend -> decode -> linear verify -> draft extend)
+for each KV dtype, and decode captured in a HIP graph and replayed with new
+lengths. Every output is checked against the float64 oracle over the pool as the
+backend left it (after its own K/V writes)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oracle
+from tests import fakes
+from tests.helpers import assert_attn_close, to_f64
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+HQ, HKV, D = 16, 2, 128
+
+
+def _backend(engine):
+    from sglang_restomod_amd.attention.mi355x.backend import MI355XAttnBackend
+
+    return MI355XAttnBackend(engine.runner)
+
+
+def _layer(kv_dtype):
+    if kv_dtype in fakes.FP8:
+        return fakes.Layer(HQ, HKV, k_scale=torch.tensor(1.5, device=DEV), v_scale=torch.tensor(0.75, device=DEV),
+                           k_scale_float=1.5, v_scale_float=0.75)
+    return fakes.Layer(HQ, HKV)
+
+
+def _pools(eng):
+    k = eng.pool.get_key_buffer(0)
+    v = eng.pool.get_value_buffer(0)
+    return to_f64(k), to_f64(v)
+
+
+def _check_extend(eng, layer, fb, q, out, prefix, ext, what):
+    kp, vp = _pools(eng)
+    r2t = eng.req_to_token.cpu().numpy()
+    rows = fb.req_pool_indices.tolist()
+    ref = oracle.extend(to_f64(q).reshape(-1, HQ, D), kp, vp, r2t, rows, prefix, ext,
+                        softmax_scale=layer.scaling, k_scale=layer.k_scale_float, v_scale=layer.v_scale_float)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    assert_attn_close(out.reshape(-1, HQ, D), ref, what=what)
+
+
+def _rand(gen, *shape, dtype=torch.bfloat16):
+    return torch.randn(*shape, generator=gen).to(dtype).to(DEV)
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float8_e5m2])
+def test_serving_sequence(kv_dtype):
+    gen = torch.Generator().manual_seed(7)
+    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=kv_dtype, pool_size=12000, max_reqs=6,
+                       context_len=4096, spec="EAGLE", topk=1)
+    layer = _layer(kv_dtype)
+    be = _backend(eng)
+    # cached prefixes computed by earlier forwards
+    prefix = {0: 300, 1: 0, 2: 1000}
+    for r, p in prefix.items():
+        if p:
+            slots = eng.alloc(r, p)
+            eng.fill(0, slots, _rand(gen, p, HKV, D), _rand(gen, p, HKV, D), layer)
+    rows = [0, 1, 2]
+    # extend (chunked prefill over the cached prefix)
+    ext = [77, 130, 5]
+    fb = eng.batch("EXTEND", rows, new_tokens=ext)
+    T = sum(ext)
+    q, k, v = _rand(gen, T, HQ * D), _rand(gen, T, HKV, D), _rand(gen, T, HKV, D)
+    be.init_forward_metadata(fb)
+    out = be.forward_extend(q, k, v, layer, fb)
+    _check_extend(eng, layer, fb, q, out, [prefix[r] for r in rows], ext, f"extend {kv_dtype}")
+    # two decode steps, batch order differing from request order
+    for step in range(2):
+        fb = eng.batch("DECODE", [2, 0, 1], new_tokens=[1, 1, 1])
+        q, k, v = _rand(gen, 3, HQ * D), _rand(gen, 3, HKV, D), _rand(gen, 3, HKV, D)
+        be.init_forward_metadata(fb)
+        out = be.forward_decode(q, k, v, layer, fb)
+        kp, vp = _pools(eng)
+        ref = oracle.decode(to_f64(q).reshape(3, HQ, D), kp, vp, eng.req_to_token.cpu().numpy(), [2, 0, 1],
+                            fb.seq_lens.tolist(), softmax_scale=layer.scaling, k_scale=layer.k_scale_float,
+                            v_scale=layer.v_scale_float)
+        assert out.shape == (3, HQ * D) and out.dtype == q.dtype
+        assert_attn_close(out.reshape(3, HQ, D), ref, what=f"decode step {step} {kv_dtype}")
+    # linear target verify: 4 draft tokens per request over the whole context
+    fb = eng.batch("TARGET_VERIFY", rows, new_tokens=[4, 4, 4], draft_token_num=4)
+    q, k, v = _rand(gen, 12, HQ * D), _rand(gen, 12, HKV, D), _rand(gen, 12, HKV, D)
+    be.init_forward_metadata(fb)
+    assert be.forward_metadata.mode == "verify"
+    out = be.forward_extend(q, k, v, layer, fb)
+    _check_extend(eng, layer, fb, q, out, fb.before, [4, 4, 4], f"verify {kv_dtype}")
+    # draft extend: a few rows per request, served by the verify kernel
+    fb = eng.batch("DRAFT_EXTEND_V2", rows, new_tokens=[3, 1, 6])
+    q, k, v = _rand(gen, 10, HQ * D), _rand(gen, 10, HKV, D), _rand(gen, 10, HKV, D)
+    be.init_forward_metadata(fb)
+    assert be.forward_metadata.mode == "verify"
+    out = be.forward_extend(q, k, v, layer, fb)
+    _check_extend(eng, layer, fb, q, out, fb.before, [3, 1, 6], f"draft extend {kv_dtype}")
+
+
+def test_sliding_window_layer_through_swa_pool():
+    gen = torch.Generator().manual_seed(11)
+    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=torch.bfloat16, pool_size=6000, max_reqs=4,
+                       context_len=2048, swa=True)
+    full = fakes.Layer(HQ, HKV, layer_id=0)
+    be = _backend(eng)
+    rows = [0, 1]
+    fb = eng.batch("EXTEND", rows, new_tokens=[400, 90])
+    T = 490
+    q, k, v = _rand(gen, T, HQ * D), _rand(gen, T, HKV, D), _rand(gen, T, HKV, D)
+    be.init_forward_metadata(fb)
+    # the SWA layer's K/V live at the translated slots of the same pool (a stand-in for
+    # the separate SWA pool): write them there, then attend through the swa table
+    swa = fakes.Layer(HQ, HKV, layer_id=0, sliding_window_size=64)
+    mapped = eng.pool.full_to_swa_index_mapping[fb.out_cache_loc]
+    eng.pool.set_kv_buffer(swa, mapped, k, v)
+    out = be.forward_extend(q, k, v, swa, fb, save_kv_cache=False)
+    kp, vp = _pools(eng)
+    swa_r2t = eng.pool.full_to_swa_index_mapping[eng.req_to_token.long()].cpu().numpy()
+    ref = oracle.extend(to_f64(q).reshape(-1, HQ, D), kp, vp, swa_r2t, rows, [0, 0], [400, 90],
+                        softmax_scale=swa.scaling, sliding_window=64)
+    assert_attn_close(out.reshape(-1, HQ, D), ref, what="swa extend")
+    del full
+
+
+def test_decode_in_a_hip_graph_replays_with_new_lengths():
+    gen = torch.Generator().manual_seed(3)
+    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=torch.bfloat16, pool_size=9000, max_reqs=8,
+                       context_len=4096)
+    layer = _layer(torch.bfloat16)
+    be = _backend(eng)
+    rows = [4, 1, 6, 0]
+    for r, n in zip(rows, [700, 33, 1500, 260]):
+        s = eng.alloc(r, n)
+        eng.fill(0, s, _rand(gen, n, HKV, D), _rand(gen, n, HKV, D), layer)
+    bs = len(rows)
+    be.init_cuda_graph_state(max_bs=8, max_num_tokens=8)
+    fb = eng.batch("DECODE", rows, new_tokens=[1] * bs)
+    eng.fill(0, fb.out_cache_loc, _rand(gen, bs, HKV, D), _rand(gen, bs, HKV, D), layer)
+    q_static = _rand(gen, bs, HQ * D)
+    be.init_forward_metadata_capture_cuda_graph(bs, bs, fb.req_pool_indices, fb.seq_lens, None,
+                                                fb.forward_mode, None)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        be.forward_decode(q_static, None, None, layer, fb, save_kv_cache=False)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_static = be.forward_decode(q_static, None, None, layer, fb, save_kv_cache=False)
+    for step in range(4):
+        # grow every request by one token (step 3 re-runs the same lengths)
+        if step < 3:
+            fb = eng.batch("DECODE", rows, new_tokens=[1] * bs)
+            eng.fill(0, fb.out_cache_loc, _rand(gen, bs, HKV, D), _rand(gen, bs, HKV, D), layer)
+        q_static.copy_(_rand(gen, bs, HQ * D))
+        be.init_forward_metadata_replay_cuda_graph(bs, fb.req_pool_indices, fb.seq_lens, fb.seq_lens_sum,
+                                                   None, fb.forward_mode, None, fb.seq_lens_cpu)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out_static.clone()
+        # eager run of the same batch between replays
+        be.init_forward_metadata(fb)
+        eager = be.forward_decode(q_static, None, None, layer, fb, save_kv_cache=False)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), f"replay {step} differs from the eager call"
+        kp, vp = _pools(eng)
+        ref = oracle.decode(to_f64(q_static).reshape(bs, HQ, D), kp, vp, eng.req_to_token.cpu().numpy(), rows,
+                            fb.seq_lens.tolist(), softmax_scale=layer.scaling)
+        assert_attn_close(got.reshape(bs, HQ, D), ref, what=f"graph replay {step}")
