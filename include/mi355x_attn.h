@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 2
+#define MA_ABI_VERSION 3
 
 /* dtype codes */
 #define MA_DT_F16 0
@@ -67,7 +67,9 @@ int ma_device_workgroups(void);
 
 /*
  * Bytes of workspace the split-KV entry points need for a persistent grid of
- * `num_workgroups` workgroups (partial results of segments shared by two waves).
+ * `num_workgroups` workgroups (1..16384): one descriptor per wave, then the partial
+ * results of segments shared by several waves. No initialisation is needed; calls
+ * that overlap in time must use different workspaces.
  */
 size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim);
 
@@ -83,8 +85,11 @@ size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim);
  *   sliding_window: -1 for none, else keys >= seq_len - 1 - window only
  *   num_workgroups: persistent grid size (ma_device_workgroups() fills the chip); the
  *     key axis of every (sequence, kv head) is cut into 32-token tiles and each wave
- *     takes an equal contiguous share of all tiles (stream-K), so ragged lengths balance
- *   workspace: ma_splitkv_workspace_bytes(num_workgroups, head_dim) bytes
+ *     takes an equal contiguous share of all tiles (stream-K, at least 2 tiles per
+ *     wave), so ragged lengths balance; a second, short kernel merges the pieces of
+ *     segments that several waves shared.
+ *   workspace: ma_splitkv_workspace_bytes(num_workgroups, head_dim) bytes, 256-byte
+ *     aligned
  *   out [batch, num_q_heads, head_dim] in q_dtype
  */
 int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,

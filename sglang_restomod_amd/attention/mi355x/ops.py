@@ -114,14 +114,15 @@ def _stream_ptr(device: torch.device) -> int:
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A growable byte buffer per (device, stream); reuse is ordered by the stream."""
+    """A growable, zero-initialised byte buffer per (device, stream); reuse is ordered by
+    the stream (the split-KV kernels need zeroed counters and leave them zeroed)."""
     if nbytes <= 0:
         return None
     key = (str(device), _stream_ptr(device))
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
         cap = 1 << max(20, (nbytes - 1).bit_length())
-        buf = torch.empty(cap, dtype=torch.uint8, device=device)
+        buf = torch.zeros(cap, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = buf
     return buf
 
@@ -132,7 +133,7 @@ def splitkv_workspace(device: torch.device, num_workgroups: Optional[int] = None
     capture graphs keep one for the graph's lifetime instead of the shared buffer)."""
     nwg = int(num_workgroups) if num_workgroups else splitkv_workgroups(device)
     nbytes = _lib.load().ma_splitkv_workspace_bytes(nwg, head_dim)
-    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    return torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
 
 
 def _splitkv_ws(lib, dev, nwg: int, D: int, given: Optional[torch.Tensor]):

@@ -49,23 +49,36 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
     return obj, proc.stderr
 
 
-def verify_inflight(src: Path, extra: list[str]) -> int:
-    """Generate the device assembly of `src` and count in-flight register hazards."""
-    from . import isa_check
-
+def _assembly(src: Path, extra: list[str]) -> Path:
+    """Device assembly of `src` (for the static checks)."""
     asm = CSRC / "_build" / (src.stem + ".s")
     cmd = [hipcc(), *common_flags(), *extra, "-S", "--cuda-device-only", str(src), "-o", str(asm)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"assembly generation failed: {' '.join(cmd)}\n{proc.stderr}")
-    return isa_check.check_file(str(asm))
+    return asm
+
+
+def verify_assembly(src: Path, asm: Path) -> None:
+    """Fail on scalar-cache writes in any kernel, and on in-flight register hazards in
+    sources whose kernels issue loads as inline assembly (marked `MA_ASM_PIPELINE`)."""
+    from . import isa_check
+
+    bad = isa_check.scalar_cache_writes(str(asm))
+    if bad:
+        raise RuntimeError(f"{src.name}: scalar-cache writes in the generated code: {sorted(set(bad))}")
+    if "MA_ASM_PIPELINE" in src.read_text():
+        hazards = isa_check.check_file(str(asm))
+        if hazards:
+            raise RuntimeError(f"{src.name}: {hazards} in-flight register hazards in the generated code "
+                               "(python -m sglang_restomod_amd.isa_check on csrc/_build/*.s lists them)")
 
 
 def build(verbose: bool = False, extra: list[str] | None = None, jobs: int | None = None) -> Path:
     """Compile every csrc/*.hip and link the shared library; returns its path.
 
-    Sources whose kernels issue loads as inline assembly (marked `MA_ASM_PIPELINE`) are
-    also checked for in-flight register hazards; any hazard fails the build.
+    The device assembly of every source is generated alongside and checked
+    (verify_assembly); a finding fails the build.
     """
     extra = list(extra or [])
     srcs = sorted(CSRC.glob("*.hip"))
@@ -73,21 +86,18 @@ def build(verbose: bool = False, extra: list[str] | None = None, jobs: int | Non
         raise RuntimeError(f"no sources under {CSRC}")
     bdir = CSRC / "_build"
     bdir.mkdir(exist_ok=True)
-    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) // 2), 8)
+    jobs = jobs or min(2 * len(srcs), max(1, (os.cpu_count() or 2) - 1), 8)
     objs = []
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_compile, s, bdir / (s.stem + ".o"), extra) for s in srcs]
+        asms = [ex.submit(_assembly, s, extra) for s in srcs]
         for f in futs:
             obj, err = f.result()
             objs.append(obj)
             if verbose and err.strip():
                 print(err, file=sys.stderr)
-    for src in srcs:
-        if "MA_ASM_PIPELINE" in src.read_text():
-            hazards = verify_inflight(src, extra)
-            if hazards:
-                raise RuntimeError(f"{src.name}: {hazards} in-flight register hazards in the generated code "
-                                   "(python -m sglang_restomod_amd.isa_check on csrc/_build/*.s lists them)")
+        for src, f in zip(srcs, asms):
+            verify_assembly(src, f.result())
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -11,8 +11,18 @@
 // range of that list. A wave walks its range, keeps an online-softmax state per segment
 // piece, writes the output directly when it covered a whole segment and a partial
 // (normalised O + log2 LSE) when the segment continues in a neighbouring wave's range.
-// A second kernel merges the partials of split segments. Ragged lengths therefore cost
-// nothing in balance, and the number of partials is at most two per wave.
+// Every wave gets at least kMinTiles tiles (small problems use fewer waves), so a segment
+// is shared by few waves. Ragged lengths cost nothing in balance, and a wave leaves at
+// most two partials: its first and its last piece.
+//
+// Merging: a shared segment ends in the first piece of the wave that holds its last
+// tile. That wave writes a small descriptor (segment, first wave, slot) for it; every
+// other wave writes an empty one. A second kernel with one wave per partial-kernel wave
+// reads its descriptor and, for a shared segment, merges the pieces of the waves that
+// shared it. The kernel boundary orders the partials before the merge (device-scope
+// fences inside one kernel would write back and invalidate whole L2 caches while other
+// waves still stream). Rows of sequences that see no key at all (no tile covers them)
+// are zeroed during the initial scan.
 //
 // A row group is 16*NB query rows of one kv head: row R -> (query token R / G,
 // GQA head R % G), so every head of a kv head is served from one read of its K/V.
@@ -26,13 +36,13 @@
 //   bf16 V: P split into two bf16 halves (exact to ~16 bits); fp16 / fp8 V: fp16 P.
 //
 // Memory pipeline: K and V of the next S-1 tiles are in flight while a tile computes
-// (S = 5 for 16-bit KV, 8 for fp8: about 250 KB per CU, which is what random 256-byte
-// row gathers need to approach HBM bandwidth). K rows land in a register ring in MFMA
-// operand layout; V rows go straight to a per-wave LDS ring by DMA (global_load_lds),
-// issued before the tile's K loads so that the compiler's wait for the K registers also
-// covers them. Slots are looked up 2S-3 tiles ahead of compute. The issue cursor clamps
+// (S = 4 for 16-bit KV, 8 for fp8: about 100-200 KB per CU; random 256-byte row gathers
+// need that much in flight to approach HBM bandwidth). K rows land in an AGPR ring in
+// MFMA operand layout; V rows go straight to a per-wave LDS ring by DMA
+// (global_load_lds). Slots are looked up 2S-3 tiles ahead of compute. All of these are
+// issued as inline assembly and waited for with explicit counts. The issue cursor clamps
 // at the wave's last tile, so the pipelined loop has no data-dependent branches around
-// loads and the compiler's wait counts stay exact.
+// loads and the counts stay exact.
 
 #include <type_traits>
 
@@ -47,6 +57,8 @@ namespace ma {
 constexpr int kWaves = 4;
 constexpr int kTile = 32;
 constexpr int kMaxRows = 32;  // 16 * NB, NB <= 2
+constexpr int kMinTiles = 2;  // least tiles per active wave
+constexpr int kDescInts = 8;  // per wave: valid, sequence, kv head, row group, first wave, its slot
 
 struct SplitKVArgs {
   const void* q;
@@ -66,13 +78,14 @@ struct SplitKVArgs {
   float scale_log2;          // softmax_scale * k_scale * log2(e)
   float v_scale;
   int nwaves;                // waves of the persistent grid
+  int* desc;                 // [nwaves][kDescInts] shared segment ending in each wave's first piece
   float* part_o;             // [nwaves][2][kMaxRows][D]
   float* part_lse;           // [nwaves][2][kMaxRows]
   void* out;
   int64_t out_stride_tok, out_stride_head;
 };
 
-// Geometry of one sequence; identical in the partial and the combine kernel.
+// Geometry of one sequence.
 struct Geom {
   int b, seq, ntok, prefix, tok0, lo_min, span, nt, rg_real;
   int64_t seq_row;
@@ -144,6 +157,59 @@ __device__ __forceinline__ void scan_work(const SplitKVArgs& a, int64_t t, int64
     base += chunk;
   }
   total = base;
+}
+
+// Zeros for every real row of sequence b (a sequence whose rows see no key: no tile
+// covers it).
+template <int D>
+__device__ __forceinline__ void write_zero_rows(const SplitKVArgs& a, int b) {
+  const Geom g = geom_u(a, b);
+  const int lane = lane_id();
+  const int n = g.ntok * a.hq * (D / 4);
+  for (int idx = lane; idx < n; idx += 64) {
+    const int row = idx / (D / 4);
+    const int d4 = (idx - row * (D / 4)) * 4;
+    const int t = row / a.hq;
+    const int h = row - t * a.hq;
+    uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) + (int64_t)(g.tok0 + t) * a.out_stride_tok +
+                             (int64_t)h * a.out_stride_head + d4;
+    *reinterpret_cast<u32x2 MA_GLOBAL*>(op) = u32x2{0u, 0u};
+  }
+}
+
+// Total tiles over all sequences. Wave W also zeroes the rows of the key-less sequences
+// b with b mod nwaves == W.
+template <int D>
+__device__ __forceinline__ int64_t scan_total(const SplitKVArgs& a, int W) {
+  const int lane = lane_id();
+  int64_t base = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int b = b0 + lane;
+    int w = 0;
+    bool zero = false;
+    if (b < a.batch) {
+      const Geom g = geom(a, b);
+      w = g.nt * g.rg_real * a.hkv;
+      zero = g.nt == 0 && g.ntok > 0 && (b % a.nwaves) == W;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) w += __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, w);
+    base += __builtin_amdgcn_readfirstlane(w);
+    uint64_t zm = __builtin_amdgcn_ballot_w64(zero);
+    while (zm) {
+      const int L = __builtin_ctzll(zm);
+      zm &= zm - 1;
+      write_zero_rows<D>(a, b0 + L);
+    }
+  }
+  return base;
+}
+
+// Waves that take part: all of them, unless that would leave a wave fewer than
+// kMinTiles tiles.
+__device__ __forceinline__ int active_waves(int64_t total, int nwaves) {
+  const int64_t want = (total + kMinTiles - 1) / kMinTiles;
+  return (int)max((int64_t)1, min((int64_t)nwaves, want));
 }
 
 // Position of a wave in its tile range: sequence geometry, kv head, row group, tile.
@@ -232,13 +298,24 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   const int j = lane >> 4;
   const int W = blockIdx.x * kWaves + wave;
 
-  int64_t total;
-  int b0, off0, bd, od;
-  scan_work(a, -1, total, bd, od);
-  const int64_t t0 = wave_begin(W, total, a.nwaves);
-  const int count = (int)(wave_begin(W + 1, total, a.nwaves) - t0);
-  if (count <= 0) return;
-  scan_work(a, t0, total, b0, off0);
+  const int64_t total = scan_total<D>(a, W);
+  const int nA = active_waves(total, a.nwaves);
+  int MA_GLOBAL* my_desc = gptr_mut(a.desc) + (int64_t)W * kDescInts;
+  if (W >= nA) {
+    if (lane == 0) my_desc[0] = 0;
+    return;
+  }
+  const int64_t t0 = wave_begin(W, total, nA);
+  const int count = (int)(wave_begin(W + 1, total, nA) - t0);
+  if (count <= 0) {
+    if (lane == 0) my_desc[0] = 0;
+    return;
+  }
+  int b0, off0;
+  {
+    int64_t tot_again;
+    scan_work(a, t0, tot_again, b0, off0);
+  }
 
   const unsigned char MA_GLOBAL* kbase = gptr(reinterpret_cast<const unsigned char*>(a.k));
   const unsigned char MA_GLOBAL* vbase = gptr(reinterpret_cast<const unsigned char*>(a.v));
@@ -326,6 +403,10 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   int lmax = 0, hmin = 0;
   bool first_piece = true;  // the current piece is the first piece of this wave's range
   int piece_start_t = 0;    // wave-local tile where the current piece began
+  // the shared segment that ends in this wave's first piece, if any
+  bool ends_shared = false;
+  int end_b = 0, end_h = 0, end_rg = 0;
+  int64_t end_first = 0;
 
   auto begin_segment = [&](const Cursor& cu) __attribute__((always_inline)) {
     const uint16_t MA_GLOBAL* qbase = gptr(reinterpret_cast<const uint16_t*>(a.q));
@@ -393,6 +474,14 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
           gptr_mut(a.part_lse)[pidx] = lt > 0.f ? __builtin_amdgcn_logf(lt) + mu * a.scale_log2 : kEmptyLse;
         }
       }
+    }
+    if (!whole && slot_sel == 0 && cu.tile == cu.g.nt - 1) {
+      // first piece of this range and last tile of its segment, which began earlier
+      ends_shared = true;
+      end_b = cu.g.b;
+      end_h = cu.h;
+      end_rg = cu.rg;
+      end_first = t0 + cu.t - cu.tile;
     }
   };
 
@@ -581,86 +670,67 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     (step(std::integral_constant<int, Is>{}, n + Is), ...);
   };
   for (int n = 0; n < count; n += S) group(std::make_integer_sequence<int, S>{}, n);
+
+  // ---- descriptor of the shared segment ending here (read by splitkv_merge) ----
+  if (lane == 0) {
+    int MA_GLOBAL* dsc = my_desc;
+    if (ends_shared) {
+      const int w1 = wave_of(end_first, total, nA);
+      dsc[1] = end_b;
+      dsc[2] = end_h;
+      dsc[3] = end_rg;
+      dsc[4] = w1;
+      dsc[5] = end_first > wave_begin(w1, total, nA) ? 1 : 0;  // slot of the first piece
+      dsc[0] = 1;
+    } else {
+      dsc[0] = 0;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Combine: one workgroup per segment (sequence, kv head, row group). Merges the
-// partial pieces of a segment that several waves shared, writes zeros for a segment
-// with real rows but no keys, and leaves whole segments (already written) alone.
+// Merge: one workgroup per partial-kernel wave W. If W's first piece ended a shared
+// segment, combine the pieces of waves w1..W into the output: a running maximum of the
+// log2 LSEs rescales the sum of the normalised partial outputs, so one pass reads each
+// piece once and the loads of successive pieces do not wait for each other's math.
+// 256 threads cover 8 rows x 128 head-dim entries per pass.
 // ---------------------------------------------------------------------------
-template <int D, bool QBF16>
-__global__ __launch_bounds__(256) void splitkv_combine(const SplitKVArgs a) {
-  const int seg = blockIdx.x;
-  const int rg = seg % a.row_groups;
-  const int h = (seg / a.row_groups) % a.hkv;
-  const int b = seg / (a.row_groups * a.hkv);
-  const Geom g = geom(a, b);
-  if (rg >= g.rg_real) return;
-  __shared__ int64_t s_red[2][256];
-  int64_t before = 0, all = 0;
-  for (int x = threadIdx.x; x < a.batch; x += 256) {
-    const int w = seq_work(a, x);
-    all += w;
-    if (x < b) before += w;
-  }
-  s_red[0][threadIdx.x] = before;
-  s_red[1][threadIdx.x] = all;
-  __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if (threadIdx.x < st) {
-      s_red[0][threadIdx.x] += s_red[0][threadIdx.x + st];
-      s_red[1][threadIdx.x] += s_red[1][threadIdx.x + st];
-    }
-    __syncthreads();
-  }
-  before = s_red[0][0];
-  const int64_t total = s_red[1][0];
-  const int rows = a.rows;
-  if (g.nt == 0) {
-    // real rows that see no key: zero output
-    for (int idx = threadIdx.x; idx < rows * D; idx += 256) {
-      const int col = idx / D, d = idx - col * D;
-      const int R = rg * rows + col;
-      const int t = R / a.group, gg = R - t * a.group;
-      if (t >= g.ntok) continue;
-      reinterpret_cast<uint16_t*>(a.out)[(int64_t)(g.tok0 + t) * a.out_stride_tok +
-                                         (int64_t)(h * a.group + gg) * a.out_stride_head + d] = 0;
-    }
-    return;
-  }
-  const int64_t first = before + (int64_t)(h * g.rg_real + rg) * g.nt;
-  const int64_t last = first + g.nt - 1;
-  const int w1 = wave_of(first, total, a.nwaves);
-  const int w2 = wave_of(last, total, a.nwaves);
-  if (w1 == w2) return;  // one wave covered the segment and wrote the output
-  const bool w1_second = first > wave_begin(w1, total, a.nwaves);
-  // 32 threads per row, 4 head-dim entries each; 8 rows per pass
-  for (int base = 0; base < rows; base += 8) {
-    const int col = base + threadIdx.x / 32;
-    const int d4 = (threadIdx.x % 32) * 4;
-    const int R = rg * rows + col;
-    const int t = R / a.group, gg = R - t * a.group;
-    if (col >= rows || t >= g.ntok) continue;
-    // waves with an empty range (more waves than tiles) hold no piece
-    float mx = -INFINITY;
-    for (int w = w1; w <= w2; ++w) {
-      if (wave_begin(w + 1, total, a.nwaves) == wave_begin(w, total, a.nwaves)) continue;
-      const int sel = (w == w1 && w1_second) ? 1 : 0;
-      mx = fmaxf(mx, a.part_lse[((int64_t)w * 2 + sel) * kMaxRows + col]);
-    }
-    float wsum = 0.f;
+template <int D, int NB, bool QBF16>
+__global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
+  const SplitKVArgs a = args;
+  constexpr int kRows = 16 * NB;
+  const int W = blockIdx.x;
+  const int MA_CONST* dsc = cptr(a.desc) + (int64_t)W * kDescInts;
+  if (dsc[0] == 0) return;
+  const int b = dsc[1], h = dsc[2], rg = dsc[3], w1 = dsc[4], sel1 = dsc[5];
+  const Geom g = geom_u(a, b);
+  const float MA_GLOBAL* plse = gptr(a.part_lse);
+  const float MA_GLOBAL* po = gptr(a.part_o);
+  const int d4 = (threadIdx.x & 31) * 4;
+#pragma unroll
+  for (int r0 = 0; r0 < kRows; r0 += 8) {
+    const int row = r0 + (threadIdx.x >> 5);
+    const int R = rg * kRows + row;
+    const int t = R / a.group;
+    const int gg = R - t * a.group;
+    if (t >= g.ntok) continue;
+    float m = -INFINITY, wsum = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int w = w1; w <= w2; ++w) {
-      if (wave_begin(w + 1, total, a.nwaves) == wave_begin(w, total, a.nwaves)) continue;
-      const int sel = (w == w1 && w1_second) ? 1 : 0;
-      const int64_t pidx = ((int64_t)w * 2 + sel) * kMaxRows + col;
-      const float wt = __builtin_amdgcn_exp2f(a.part_lse[pidx] - mx);
-      wsum += wt;
-      acc += *reinterpret_cast<const f32x4*>(a.part_o + pidx * D + d4) * wt;
+#pragma unroll 4
+    for (int w = w1; w <= W; ++w) {
+      const int64_t pidx = ((int64_t)w * 2 + (w == w1 ? sel1 : 0)) * kMaxRows + row;
+      const float lse = plse[pidx];
+      const f32x4 o = *reinterpret_cast<const f32x4 MA_GLOBAL*>(po + pidx * D + d4);
+      const float m_new = fmaxf(m, lse);  // every LSE is finite (empty pieces: -2^30)
+      const float s_old = __builtin_amdgcn_exp2f(m - m_new);
+      const float s_new = __builtin_amdgcn_exp2f(lse - m_new);
+      acc = acc * s_old + o * s_new;
+      wsum = wsum * s_old + s_new;
+      m = m_new;
     }
-    uint16_t* op = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(g.tok0 + t) * a.out_stride_tok +
-                   (int64_t)(h * a.group + gg) * a.out_stride_head + d4;
-    *reinterpret_cast<u32x2*>(op) = pack4<QBF16>(acc, a.v_scale / wsum);
+    uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) + (int64_t)(g.tok0 + t) * a.out_stride_tok +
+                             (int64_t)(h * a.group + gg) * a.out_stride_head + d4;
+    *reinterpret_cast<u32x2 MA_GLOBAL*>(op) = pack4<QBF16>(acc, a.v_scale / wsum);
   }
 }
 
@@ -696,12 +766,23 @@ static int device_workgroups(int requested) {
   return cus;
 }
 
+// Workspace: [descriptors: nwaves x kDescInts int32][partial O: nwaves x 2 x 32 x D fp32]
+// [LSE: nwaves x 2 x 32 fp32], each region 256-byte aligned. Every call rewrites the
+// descriptors of all its waves, so the workspace needs no initialisation.
+constexpr int kMaxWorkgroups = 16384;
+static size_t ws_desc_bytes(int num_workgroups) {
+  return ((size_t)num_workgroups * kWaves * kDescInts * sizeof(int) + 255) & ~(size_t)255;
+}
+static size_t ws_o_bytes(int num_workgroups, int head_dim) {
+  const size_t pieces = (size_t)num_workgroups * kWaves * 2 * kMaxRows;
+  return (pieces * head_dim * sizeof(float) + 255) & ~(size_t)255;
+}
+
 extern "C" size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim) {
   if (num_workgroups <= 0 || head_dim <= 0) return 0;
   const size_t pieces = (size_t)num_workgroups * kWaves * 2 * kMaxRows;
-  size_t o = pieces * head_dim * sizeof(float);
-  o = (o + 255) & ~(size_t)255;
-  return o + ((pieces * sizeof(float) + 255) & ~(size_t)255);
+  return ws_desc_bytes(num_workgroups) + ws_o_bytes(num_workgroups, head_dim) +
+         ((pieces * sizeof(float) + 255) & ~(size_t)255);
 }
 
 extern "C" int ma_device_workgroups(void) { return device_workgroups(0); }
@@ -718,7 +799,8 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
   if (!(a.scale_log2 > 0.f)) return set_error(MA_EINVAL, "softmax scale must be positive");
   if (a.tt.page_shift < 0 || a.tt.page_shift > 16) return set_error(MA_EINVAL, "bad page shift");
   if (max_q_per_seq <= 0) return set_error(MA_EINVAL, "max query rows per sequence must be positive");
-  if (num_workgroups <= 0) return set_error(MA_EINVAL, "num_workgroups must be positive (ma_device_workgroups())");
+  if (num_workgroups <= 0 || num_workgroups > kMaxWorkgroups)
+    return set_error(MA_EINVAL, "num_workgroups must be in 1..%d (ma_device_workgroups())", kMaxWorkgroups);
   if (a.batch == 0) return MA_OK;
   if (!a.q || !a.k || !a.v || !a.tt.table || !a.seq_lens || !a.out)
     return set_error(MA_EINVAL, "null pointer argument");
@@ -738,18 +820,25 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
   const size_t need = ma_splitkv_workspace_bytes(num_workgroups, head_dim);
   if (!workspace || workspace_bytes < need)
     return set_error(MA_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
-  const size_t pieces = (size_t)num_workgroups * kWaves * 2 * kMaxRows;
-  const size_t o_bytes = (pieces * head_dim * sizeof(float) + 255) & ~(size_t)255;
-  a.part_o = reinterpret_cast<float*>(workspace);
-  a.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + o_bytes);
+  char* ws = reinterpret_cast<char*>(workspace);
+  if (reinterpret_cast<uintptr_t>(ws) & 255) return set_error(MA_EINVAL, "workspace must be 256-byte aligned");
+  a.desc = reinterpret_cast<int*>(ws);
+  a.part_o = reinterpret_cast<float*>(ws + ws_desc_bytes(num_workgroups));
+  a.part_lse = reinterpret_cast<float*>(ws + ws_desc_bytes(num_workgroups) + ws_o_bytes(num_workgroups, head_dim));
   const int64_t segs = (int64_t)a.batch * a.hkv * a.row_groups;
   if (segs > 0x7fffffff) return set_error(MA_EINVAL, "too many segments");
   hipError_t e = launch_partial_d<128>(nb, q_dtype == DT_BF16, kv_dtype, dim3(num_workgroups), stream, a);
-  if (e != hipSuccess) return set_error(MA_ELAUNCH, "partial launch failed: %s", hipGetErrorString(e));
-  if (q_dtype == DT_BF16) hipLaunchKernelGGL((splitkv_combine<128, true>), dim3((unsigned)segs), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((splitkv_combine<128, false>), dim3((unsigned)segs), dim3(256), 0, stream, a);
+  if (e != hipSuccess) return set_error(MA_ELAUNCH, "split-KV launch failed: %s", hipGetErrorString(e));
+  const dim3 mgrid((unsigned)a.nwaves);  // one workgroup per partial-kernel wave
+  if (q_dtype == DT_BF16) {
+    if (nb == 1) hipLaunchKernelGGL((splitkv_merge<128, 1, true>), mgrid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((splitkv_merge<128, 2, true>), mgrid, dim3(256), 0, stream, a);
+  } else {
+    if (nb == 1) hipLaunchKernelGGL((splitkv_merge<128, 1, false>), mgrid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((splitkv_merge<128, 2, false>), mgrid, dim3(256), 0, stream, a);
+  }
   e = hipGetLastError();
-  if (e != hipSuccess) return set_error(MA_ELAUNCH, "combine launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return set_error(MA_ELAUNCH, "merge launch failed: %s", hipGetErrorString(e));
   return MA_OK;
 }
 

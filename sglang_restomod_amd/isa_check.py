@@ -54,6 +54,17 @@ def check(body, name):
             issued += 1
     return problems
 
+# Writes through the scalar data cache (scalar stores and atomics, and that cache's
+# write-back / discard) must never appear in this library's kernels.
+SCALAR_CACHE_WRITES = re.compile(r"^\s*(s_store|s_buffer_store|s_scratch_store|s_atomic|s_buffer_atomic|"
+                                 r"s_dcache_wb|s_dcache_discard)\w*", re.M)
+
+
+def scalar_cache_writes(path):
+    """Lines of an assembly listing that write through the scalar data cache."""
+    return [m.group(0).strip() for m in SCALAR_CACHE_WRITES.finditer(open(path).read())]
+
+
 def check_file(path, verbose=False):
     """Return the number of hazards over all kernels of an assembly listing."""
     s = open(path).read()
