@@ -5,32 +5,45 @@
 // _paged_adapter.py:567-759): query token i of sequence b sees key j when
 //   j < seq_lens[b]  and (causal: j <= prefix[b] + i)  and (window W >= 0: j >= prefix[b] + i - W).
 //
-// Decomposition: one workgroup = 4 waves = 128 query rows of ONE kv head, where row
-// r of a sequence is (query token r / G, GQA head r % G). All G heads that share a
-// kv head therefore share each K/V tile staged in LDS (GQA read once per tile).
-// Row tiles are launched heaviest-first (the last tokens of a causal sequence see
-// the most keys).
+// Decomposition: one workgroup = 8 waves = 256 query rows of ONE kv head, where row r of
+// a sequence is (query token r / G, GQA head r % G); each wave owns 32 rows (two 16-row
+// blocks), two waves per SIMD so that one's softmax overlaps the other's MFMAs. All G
+// heads that share a kv head are served from one copy of each K/V tile in LDS. Row tiles
+// are launched heaviest-first (the last tokens of a causal sequence see the most keys).
 //
-// Per 64-key tile, per wave (32 rows = two 16-row blocks), MFMA 16x16x32:
-//   S^T[key, row] = K[key, :] . Q[row, :]   A = K from LDS (row-major, padded rows),
-//                                           B = Q^T held in registers for the whole kernel.
-//   O^T[d, row] += V^T[d, key] P^T[key, row] A = V^T from LDS (head-dim rows, keys in the
-//                                           order the S^T accumulator holds them), B = P^T
-//                                           straight from the S^T accumulators (fp16).
-// K/V rows of tile n+1 are gathered from HBM into registers while tile n computes.
-// bf16/fp16 K stays in the query dtype (exact products); V is converted to fp16 when
-// staged (exact for |v| < 65504) and P is fp16, fp32 accumulate, fp32 softmax state.
+// Per 64-key tile, per wave, MFMA 16x16x32 with fp32 accumulate:
+//   S^T[key, row] = K[key, :] . Q[row, :]     A = K from LDS, B = Q^T (registers, whole kernel)
+//   O^T[d, row] += V^T[d, key] P^T[key, row]  A = V^T read transposed from LDS
+//                                             (ds_read_b64_tr_b16 / _tr_b8), B = P^T straight
+//                                             from the S^T accumulators, in fp16.
+// K stays in the query dtype (exact products; fp8 converted exactly). V is used in fp16:
+// bf16 V is converted in LDS once per tile (each wave converts the part it loaded, exact
+// for |v| in fp16's normal range), fp8 V exactly while it is read. P is fp16, the
+// softmax state fp32.
+//
+// Memory pipeline: K and V tiles travel HBM -> LDS by DMA (global_load_lds) into an
+// S-stage ring, with S-1 tiles in flight while one computes; each wave moves an eighth
+// of every tile. K lands as MFMA fragment blocks (block (kb, kk) = 16 keys x 8 head-dim
+// entries, lane l's 16 bytes at l * 16), so each operand read is one conflict-free
+// ds_read_b128; V lands row-major with an XOR swizzle of its 16-byte chunks. Slots are
+// looked up S+1 tiles ahead. The loads are inline assembly with explicit wait counts,
+// and one barrier per tile both publishes a tile and retires the stage it replaces.
+
+#include <type_traits>
 
 #include "common.h"
+
+// MA_ASM_PIPELINE: the build verifies the generated code of this file for accesses to
+// registers whose inline-assembly loads are still in flight.
 #include "capi_internal.h"
 
 namespace ma {
 
-constexpr int kXBM = 128;              // query rows per workgroup
-constexpr int kXBN = 64;               // keys per tile
-constexpr int kXD = 128;               // head dim
-constexpr int kKRow = kXD * 2 + 16;    // bytes per K row in LDS (padded)
-constexpr int kVRow = kXBN * 2 + 16;   // bytes per V^T row in LDS (padded)
+constexpr int kXWaves = 8;                     // waves per workgroup
+constexpr int kXRB = 2;                        // 16-row blocks per wave
+constexpr int kXBM = kXWaves * kXRB * 16;      // query rows per workgroup
+constexpr int kXBN = 64;                       // keys per tile
+constexpr int kXD = 128;                       // head dim
 
 struct ExtendArgs {
   const void* q;
@@ -52,294 +65,344 @@ struct ExtendArgs {
   int64_t out_stride_tok, out_stride_head;
 };
 
-// Column of the V^T tile that holds tile-local key `key` (0..63): within each 32-key
-// step, keys 4j..4j+3 -> columns 8j..8j+3 and keys 16+4j..16+4j+3 -> columns 8j+4..8j+7,
-// the order in which the S^T accumulators of lane group j hold them.
-__device__ __forceinline__ int vt_col(int key) {
-  const int step = key >> 5, k = key & 31;
-  const int blk = k >> 4, jj = (k >> 2) & 3, i = k & 3;
-  return step * 32 + jj * 8 + blk * 4 + i;
-}
-
 template <bool QBF16, int KV>
-__global__ __launch_bounds__(256) void extend_kernel(const ExtendArgs a) {
+__global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArgs args) {
+  const ExtendArgs a = args;  // local copy: the lambdas capture by reference
   constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
-  __shared__ __attribute__((aligned(16))) unsigned char ks[kXBN * kKRow];
-  __shared__ __attribute__((aligned(16))) unsigned char vs[kXD * kVRow];
+  constexpr bool kConvV = (!kFp8) && QBF16;      // bf16 V: converted to fp16 in LDS
+  constexpr int kElt = kFp8 ? 1 : 2;
+  constexpr int kKSub = kFp8 ? 2 : 4;            // K DMA blocks per 16-key block
+  constexpr int kRowB = kXD * kElt;              // bytes of one K/V row
+  constexpr int kStageB = kXBN * kRowB;          // bytes of the K (or V) part of a tile
+  constexpr int kKBlk = kStageB / 1024 / kXWaves;  // K DMA blocks per wave per tile
+  constexpr int kVBlk = kStageB / 1024 / kXWaves;  // V DMA blocks per wave per tile
+  constexpr int ND = kKBlk + kVBlk;              // DMA instructions per wave per tile
+  constexpr int OPS = 1 + ND;                    // plus one slot lookup
+  constexpr int S = 4;                           // pipeline stages
+  constexpr int A = S + 1;                       // slot lookahead (tiles)
+  static_assert((S - 1) * ND + 2 <= 63, "outstanding loads exceed the counter");
+  static_assert(kKBlk >= 1 && kKSub % kKBlk == 0, "a wave's K blocks share one key block");
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  __shared__ __attribute__((aligned(1024))) unsigned char kring[S][kStageB];
+  __shared__ __attribute__((aligned(1024))) unsigned char vring[S][kStageB];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
   const int j = lane >> 4;
 
   const int rt = a.row_tiles - 1 - (int)blockIdx.x;  // heaviest row tiles first
   const int h = blockIdx.y;
   const int b = blockIdx.z;
-  const int tok0 = a.qsl[b];
-  const int ntok = a.qsl[b + 1] - tok0;
+  const int tok0 = cptr(a.qsl)[b];
+  const int ntok = cptr(a.qsl)[b + 1] - tok0;
   const int r0 = rt * kXBM;
   if (r0 >= ntok * a.group) return;
-  const int seq = a.seq_lens[b];
-  const int prefix = a.prefix ? a.prefix[b] : seq - ntok;
-  const int64_t seq_row = a.row_index ? a.row_index[b] : (int64_t)b;
+  const int seq = cptr(a.seq_lens)[b];
+  const int prefix = a.prefix ? cptr(a.prefix)[b] : seq - ntok;
+  const int64_t seq_row = a.row_index ? cptr(a.row_index)[b] : (int64_t)b;
 
-  // ---- rows of this lane (one per 16-row block of the wave) ----
-  int lo_r[2], hi_r[2];
-  bool real[2];
-  u32x4 qv[2][4];
-  const uint16_t* qbase = reinterpret_cast<const uint16_t*>(a.q);
+  // ---- this lane's rows (one per 16-row block) ----
+  int lo_r[kXRB], hi_r[kXRB];
+  bool real[kXRB];
+  u32x4 qv[kXRB][4];
+  const uint16_t MA_GLOBAL* qbase = gptr(reinterpret_cast<const uint16_t*>(a.q));
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int r = r0 + wave * 32 + rb * 16 + c;
+  for (int rb = 0; rb < kXRB; ++rb) {
+    const int r = r0 + wave * (kXRB * 16) + rb * 16 + c;
     const int t = r / a.group;
     const int g = r - t * a.group;
     real[rb] = t < ntok;
     const int qpos = prefix + t;
     lo_r[rb] = (real[rb] && a.window >= 0) ? max(0, qpos - a.window) : 0;
     hi_r[rb] = real[rb] ? (a.causal ? min(seq, qpos + 1) : seq) : 0;
-    const uint16_t* qp = qbase + (int64_t)(tok0 + t) * a.q_stride_tok + (int64_t)(h * a.group + g) * a.q_stride_head + j * 32;
+    const uint16_t MA_GLOBAL* qp =
+        qbase + (int64_t)(tok0 + t) * a.q_stride_tok + (int64_t)(h * a.group + g) * a.q_stride_head + j * 32;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      qv[rb][kk] = real[rb] ? *reinterpret_cast<const u32x4*>(qp + kk * 8) : u32x4{0, 0, 0, 0};
+      qv[rb][kk] = real[rb] ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + kk * 8) : u32x4{0, 0, 0, 0};
   }
-  // key range of the whole workgroup and the window in which no row needs masking
+  // keys any row of the workgroup may see, and the window in which no row needs masking
   const int t_first = r0 / a.group;
   const int t_last = min(ntok - 1, (r0 + kXBM - 1) / a.group);
   const int key_lo = a.window >= 0 ? max(0, prefix + t_first - a.window) : 0;
   const int key_hi = a.causal ? min(seq, prefix + t_last + 1) : seq;
   const int full_lo = a.window >= 0 ? max(0, prefix + t_last - a.window) : 0;
   const int full_hi = a.causal ? min(seq, prefix + t_first + 1) : seq;
+  const int ntiles = key_hi > key_lo ? (key_hi - key_lo + kXBN - 1) / kXBN : 0;
 
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
-  f32x4 o[2][8];
+  float m_run[kXRB], l_run[kXRB];
+  f32x4 o[kXRB][8];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < kXRB; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.f;
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const unsigned char* kbase = reinterpret_cast<const unsigned char*>(a.k);
-  const unsigned char* vbase = reinterpret_cast<const unsigned char*>(a.v);
-  constexpr int kElt = kFp8 ? 1 : 2;
-  const int64_t row_bytes = a.kv_stride_row * kElt;
-  const int64_t head_off = (int64_t)h * a.kv_stride_head * kElt;
-
-  // ---- global -> register staging of one tile ----
-  // 16-bit: K: thread loads chunk (tid & 15) of keys (tid >> 4) + 16 i;
-  //         V: thread loads chunk (tid & 15) of keys 4 (tid >> 4) + i.
-  // fp8:    K: chunk (tid & 7) of keys (tid >> 3) + 32 i (i < 2);
-  //         V: chunk (tid & 7) of keys 2 (tid >> 3) + i (i < 2).
-  u32x4 kreg[4], vreg[4];
-  auto load_tile = [&](int base) {
-    if constexpr (kFp8) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int key = (tid >> 3) + 32 * i;
-        const int pos = base + key;
-        if (pos < key_hi) {
-          const int64_t row = kv_row(a.tt, seq_row, pos);
-          kreg[i] = *reinterpret_cast<const u32x4*>(kbase + row * row_bytes + head_off + (tid & 7) * 16);
-        } else {
-          kreg[i] = u32x4{0, 0, 0, 0};
-        }
-        const int vkey = 2 * (tid >> 3) + i;
-        const int vpos = base + vkey;
-        if (vpos < key_hi) {
-          const int64_t row = kv_row(a.tt, seq_row, vpos);
-          vreg[i] = *reinterpret_cast<const u32x4*>(vbase + row * row_bytes + head_off + (tid & 7) * 16);
-        } else {
-          vreg[i] = u32x4{0, 0, 0, 0};
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = (tid >> 4) + 16 * i;
-        const int pos = base + key;
-        if (pos < key_hi) {
-          const int64_t row = kv_row(a.tt, seq_row, pos);
-          kreg[i] = *reinterpret_cast<const u32x4*>(kbase + row * row_bytes + head_off + (tid & 15) * 16);
-        } else {
-          kreg[i] = u32x4{0, 0, 0, 0};
-        }
-        const int vkey = 4 * (tid >> 4) + i;
-        const int vpos = base + vkey;
-        if (vpos < key_hi) {
-          const int64_t row = kv_row(a.tt, seq_row, vpos);
-          vreg[i] = *reinterpret_cast<const u32x4*>(vbase + row * row_bytes + head_off + (tid & 15) * 16);
-        } else {
-          vreg[i] = u32x4{0, 0, 0, 0};
-        }
-      }
-    }
-  };
-
-  // ---- register -> LDS (K row-major in the query dtype, V^T in fp16) ----
-  auto store_tile = [&]() {
-    if constexpr (kFp8) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int key = (tid >> 3) + 32 * i;
-        u32x4 lo, hi;
-        cvt16_fp8<KV, QBF16>(kreg[i], lo, hi);
-        unsigned char* dst = ks + key * kKRow + (tid & 7) * 32;
-        *reinterpret_cast<u32x4*>(dst) = lo;
-        *reinterpret_cast<u32x4*>(dst + 16) = hi;
-      }
-      // V: two keys x 16 head-dim entries -> 16 packed pairs
-      u32x4 v0l, v0h, v1l, v1h;
-      cvt16_fp8<KV, false>(vreg[0], v0l, v0h);
-      cvt16_fp8<KV, false>(vreg[1], v1l, v1h);
-      const int col = vt_col(2 * (tid >> 3));
-      const int d0 = (tid & 7) * 16;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int w = e >> 1;
-        const uint32_t a0 = (w < 4) ? v0l[w] : v0h[w - 4];
-        const uint32_t a1 = (w < 4) ? v1l[w] : v1h[w - 4];
-        const uint32_t pk = (e & 1) ? pack_hi(a0, a1) : pack_lo(a0, a1);
-        *reinterpret_cast<uint32_t*>(vs + (d0 + e) * kVRow + col * 2) = pk;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = (tid >> 4) + 16 * i;
-        *reinterpret_cast<u32x4*>(ks + key * kKRow + (tid & 15) * 16) = kreg[i];
-      }
-      // V: 4 keys x 8 head-dim entries; bf16 -> fp16 (exact in range), transpose in registers
-      uint32_t vh[4][4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          if constexpr (QBF16) {
-            const uint32_t x = vreg[i][w];
-            vh[i][w] = pack_f16(__builtin_bit_cast(float, x << 16), __builtin_bit_cast(float, x & 0xffff0000u));
-          } else {
-            vh[i][w] = vreg[i][w];
-          }
-        }
-      const int col = vt_col(4 * (tid >> 4));
-      const int d0 = (tid & 15) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int w = e >> 1;
-        u32x2 pk;
-        if (e & 1) { pk[0] = pack_hi(vh[0][w], vh[1][w]); pk[1] = pack_hi(vh[2][w], vh[3][w]); }
-        else { pk[0] = pack_lo(vh[0][w], vh[1][w]); pk[1] = pack_lo(vh[2][w], vh[3][w]); }
-        *reinterpret_cast<u32x2*>(vs + (d0 + e) * kVRow + col * 2) = pk;
-      }
-    }
-  };
-
-  if (key_lo < key_hi) load_tile(key_lo);
-  for (int base = key_lo; base < key_hi; base += kXBN) {
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (base + kXBN < key_hi) load_tile(base + kXBN);
-
-    // ---- S^T = K Q^T : 4 key blocks x 2 row blocks ----
-    f32x4 s[2][4];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) s[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + (kb * 16 + c) * kKRow + (j * 32 + kk * 8) * 2);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) s[rb][kb] = mfma16t<QBF16>(kf, qv[rb][kk], s[rb][kb]);
-      }
-    }
-
-    // ---- online softmax per row (lane column) ----
-    const bool full = (base >= full_lo) && (base + kXBN <= full_hi);
-    u32x4 pk[2][2];
-    float alpha[2];
-    bool grew = false;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      if (!full) {
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int pos = base + kb * 16 + 4 * j + i;
-            if (pos < lo_r[rb] || pos >= hi_r[rb]) s[rb][kb][i] = -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-        mx = fmaxf(mx, fmaxf(fmaxf(s[rb][kb][0], s[rb][kb][1]), fmaxf(s[rb][kb][2], s[rb][kb][3])));
-      mx = fmaxf(mx, shfl_xor_f(mx, 16));
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
-      const float m_new = fmaxf(m_run[rb], mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      grew |= (m_new != m_run[rb]);
-      alpha[rb] = __builtin_amdgcn_exp2f((m_run[rb] - m_use) * a.scale_log2);
-      m_run[rb] = m_new;
-      const float msc = m_use * a.scale_log2;
-      float p[16];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p[kb * 4 + i] = __builtin_amdgcn_exp2f(s[rb][kb][i] * a.scale_log2 - msc);
-      float ps = 0.f;
-#pragma unroll
-      for (int x = 0; x < 16; ++x) ps += p[x];
-      l_run[rb] = l_run[rb] * alpha[rb] + ps;
-      // P^T operand for key step ks: keys (2ks block, i) then (2ks+1 block, i)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        pk[rb][st][0] = pack_f16(p[(2 * st) * 4 + 0], p[(2 * st) * 4 + 1]);
-        pk[rb][st][1] = pack_f16(p[(2 * st) * 4 + 2], p[(2 * st) * 4 + 3]);
-        pk[rb][st][2] = pack_f16(p[(2 * st + 1) * 4 + 0], p[(2 * st + 1) * 4 + 1]);
-        pk[rb][st][3] = pack_f16(p[(2 * st + 1) * 4 + 2], p[(2 * st + 1) * 4 + 3]);
-      }
-    }
-    if (__builtin_amdgcn_ballot_w64(grew)) {
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int db = 0; db < 8; ++db) o[rb][db] *= alpha[rb];
-    }
-
-    // ---- O^T += V^T P^T : 8 head-dim blocks x 2 key steps x 2 row blocks ----
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const u32x4 vf = *reinterpret_cast<const u32x4*>(vs + (db * 16 + c) * kVRow + (st * 32 + j * 8) * 2);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) o[rb][db] = mfma16t<false>(vf, pk[rb][st], o[rb][db]);
-      }
-    }
   }
 
-  // ---- epilogue: normalise and write this lane's row ----
+  const unsigned char MA_GLOBAL* kbase = gptr(reinterpret_cast<const unsigned char*>(a.k));
+  const unsigned char MA_GLOBAL* vbase = gptr(reinterpret_cast<const unsigned char*>(a.v));
+  const int64_t row_bytes = a.kv_stride_row * kElt;
+  const int64_t head_off = (int64_t)h * a.kv_stride_head * kElt;
+  auto swz = [](int t) -> int { return kFp8 ? ((t & 3) | ((t >> 2) & 4)) : ((2 * t) & 15); };
+
+  // ---- memory pipeline ----
+  // Lane l looks up the slot of key l of a tile; tiles past the last are clamped to it
+  // (their loads are issued and ignored, so every step issues the same instructions).
+  auto key_of = [&](int tile) __attribute__((always_inline)) -> int {
+    return min(key_lo + min(tile, ntiles - 1) * kXBN + lane, key_hi - 1);
+  };
+  auto load_slot = [&](int tile) __attribute__((always_inline)) -> int {
+    const int pos = key_of(tile);
+    const int32_t MA_GLOBAL* tp = gptr(a.tt.table) + seq_row * a.tt.stride + (pos >> a.tt.page_shift);
+    int page;
+    __asm__ volatile("global_load_dword %0, %1, off" : "=v"(page) : "v"(tp) : "memory");
+    return page;
+  };
+  auto slot_of = [&](int tile, int page) __attribute__((always_inline)) -> int {
+    const int pos = key_of(tile);
+    return (page << a.tt.page_shift) | (pos & ((1 << a.tt.page_shift) - 1));
+  };
+  auto dma = [&](const unsigned char MA_GLOBAL* src, uint32_t lds) __attribute__((always_inline)) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+    __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
+  };
+  auto issue = [&](int myslot, int st) __attribute__((always_inline)) {
+    const uint32_t kl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)kring[st];
+    const uint32_t vl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)vring[st];
+    // all slot shuffles first, so that their LDS round trips overlap; this wave's K blocks
+    // (kb, sub) = divmod(wave * kKBlk + x, kKSub) all lie in key block kb
+    const int kb_w = (wave * kKBlk) / kKSub;
+    const int kslot = shfl_i(myslot, kb_w * 16 + c);
+    int vslot[kVBlk];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+    for (int x = 0; x < kVBlk; ++x) {
+      const int xb = wave * kVBlk + x;
+      vslot[x] = shfl_i(myslot, kFp8 ? (8 * xb + (lane >> 3)) : (4 * xb + (lane >> 4)));
+    }
+    // K: lane l -> key kb_w*16 + (l & 15), 16-byte chunk kKSub*j + sub
+    const unsigned char MA_GLOBAL* kp = kbase + (int64_t)kslot * row_bytes + head_off;
+#pragma unroll
+    for (int x = 0; x < kKBlk; ++x) {
+      const int blk = wave * kKBlk + x;
+      dma(kp + (kKSub * j + blk % kKSub) * 16, kl + blk * 1024);
+    }
+    // V: rows of this wave's blocks, row-major, 16-byte chunks XOR-swizzled by row
+#pragma unroll
+    for (int x = 0; x < kVBlk; ++x) {
+      const int xb = wave * kVBlk + x;
+      const int tok = kFp8 ? (8 * xb + (lane >> 3)) : (4 * xb + (lane >> 4));
+      const int pos = kFp8 ? (lane & 7) : (lane & 15);
+      dma(vbase + (int64_t)vslot[x] * row_bytes + head_off + ((pos ^ swz(tok)) << 4), vl + xb * 1024);
+    }
+  };
+  auto wait_vm = [&](auto N_) __attribute__((always_inline)) {
+    constexpr int N = decltype(N_)::value;
+    __asm__ volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+  };
+  auto barrier = [&]() __attribute__((always_inline)) { __asm__ volatile("s_barrier" : : : "memory"); };
+  // bf16 V -> fp16 in place, the 16 bytes per block that this lane loaded
+  auto convert_v = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int x = 0; x < kVBlk; ++x) {
+      u32x4* pv = reinterpret_cast<u32x4*>(vring[st] + (wave * kVBlk + x) * 1024 + lane * 16);
+      u32x4 v = *pv;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        v[w] = pack_f16(__builtin_bit_cast(float, v[w] << 16), __builtin_bit_cast(float, v[w] & 0xffff0000u));
+      *pv = v;
+    }
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  // per-lane part of the V^T read addresses (16-bit V): row 4j + e, column bits of cc
+  const int vrow = (4 * j + (c >> 2)) * kRowB + ((lane & 3) >> 1) * 16 + (lane & 1) * 8;
+  const int vs1 = (4 * j + (c >> 2)) & 7;
+
+  // ---- one tile, as two 32-key halves (scores, softmax and PV per half) ----
+  auto compute = [&](int tile, int st) __attribute__((always_inline)) {
+    const unsigned char* kt = kring[st];
+    const unsigned char* vt = vring[st];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int base = key_lo + tile * kXBN + hf * 32;
+      // S^T = K Q^T: key blocks 2hf, 2hf+1 x 4 row blocks
+      f32x4 s[kXRB][2];
+#pragma unroll
+      for (int rb = 0; rb < kXRB; ++rb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) s[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (kFp8) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(kt + ((2 * hf + kb) * 2 + hh) * 1024 + lane * 16);
+            u32x4 k0, k1;
+            cvt16_fp8<KV, QBF16>(raw, k0, k1);
+#pragma unroll
+            for (int rb = 0; rb < kXRB; ++rb) {
+              s[rb][kb] = mfma16t<QBF16>(k0, qv[rb][2 * hh], s[rb][kb]);
+              s[rb][kb] = mfma16t<QBF16>(k1, qv[rb][2 * hh + 1], s[rb][kb]);
+            }
+          }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            const u32x4 kf = *reinterpret_cast<const u32x4*>(kt + ((2 * hf + kb) * 4 + kk) * 1024 + lane * 16);
+#pragma unroll
+            for (int rb = 0; rb < kXRB; ++rb) s[rb][kb] = mfma16t<QBF16>(kf, qv[rb][kk], s[rb][kb]);
+          }
+      }
+      // online softmax per row (lane column)
+      const bool full = (base >= full_lo) && (base + 32 <= full_hi);
+      u32x4 pk[kXRB];
+      float alpha[kXRB];
+      bool grew = false;
+#pragma unroll
+      for (int rb = 0; rb < kXRB; ++rb) {
+        if (!full) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int pos = base + kb * 16 + 4 * j + i;
+              if (pos < lo_r[rb] || pos >= hi_r[rb]) s[rb][kb][i] = -INFINITY;
+            }
+        }
+        float mx = fmaxf(fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), fmaxf(s[rb][0][2], s[rb][0][3])),
+                         fmaxf(fmaxf(s[rb][1][0], s[rb][1][1]), fmaxf(s[rb][1][2], s[rb][1][3])));
+        // the row maximum only changes if some lane holds a score above it: then (and
+        // only then) reduce across the four lanes of each row
+        alpha[rb] = 1.f;
+        if (__builtin_amdgcn_ballot_w64(mx > m_run[rb])) {
+          mx = fmaxf(mx, shfl_xor_f(mx, 16));
+          mx = fmaxf(mx, shfl_xor_f(mx, 32));
+          const float m_new = fmaxf(m_run[rb], mx);
+          const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+          grew |= (m_new != m_run[rb]);
+          alpha[rb] = __builtin_amdgcn_exp2f((m_run[rb] - m_use) * a.scale_log2);
+          m_run[rb] = m_new;
+        }
+        const float m_use = (m_run[rb] == -INFINITY) ? 0.f : m_run[rb];
+        const float msc = m_use * a.scale_log2;
+        float p[8];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[kb * 4 + i] = __builtin_amdgcn_exp2f(s[rb][kb][i] * a.scale_log2 - msc);
+        const float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        l_run[rb] = l_run[rb] * alpha[rb] + ps;
+        // P^T operand: keys of block 2hf (4j+i), then of block 2hf+1 (16+4j+i)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pk[rb][w] = pack_f16(p[2 * w], p[2 * w + 1]);
+      }
+      if (__builtin_amdgcn_ballot_w64(grew)) {
+#pragma unroll
+        for (int rb = 0; rb < kXRB; ++rb)
+#pragma unroll
+          for (int db = 0; db < 8; ++db) o[rb][db] *= alpha[rb];
+      }
+      // O^T += V^T P^T: 8 head-dim blocks x 4 row blocks
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        u32x4 va;
+        if constexpr (kFp8) {
+          const int e = c >> 1, cc = lane & 1;
+          const int t = hf * 32 + ((e < 4) ? (4 * j + e) : (16 + 4 * j + e - 4));
+          const unsigned char* ptr = vt + t * kRowB + ((db ^ swz(t)) << 4) + cc * 8;
+          const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (__attribute__((address_space(3))) i32x2*)(ptr)));
+          va = cvt8_fp8<KV, false>(raw[0], raw[1]);
+        } else {
+          // row t = hf*32 + 16*half + 4j + e; its swizzle is lane-constant (t & 7 = vs1), so
+          // chunk (2db + cc/2) ^ swz(t) = 2 (db ^ vs1) + cc/2
+          const unsigned char* pcol = vt + vrow + ((db ^ vs1) << 5);
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const unsigned char* ptr = pcol + (hf * 32 + 16 * half) * kRowB;
+            const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(ptr)));
+            va[2 * half] = raw[0];
+            va[2 * half + 1] = raw[1];
+          }
+        }
+#pragma unroll
+        for (int rb = 0; rb < kXRB; ++rb) o[rb][db] = mfma16t<false>(va, pk[rb], o[rb][db]);
+      }
+    }
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+
+  // ---- schedule ----
+  // Step k: look up the slots of tile k+A; once the slots of tile k+S-1 (looked up at
+  // step k-2) have landed, and at k >= 0 after a barrier, issue tile k+S-1 into stage
+  // (k+S-1) % S; at k >= 0 compute tile k from stage k % S. Steps -A..-1 are the
+  // prologue. Instructions issued per step: one slot lookup, plus ND from step 1-S on.
+  auto nd_at = [](int k) constexpr -> int { return k >= 1 - S ? ND : 0; };
+  auto wait_at = [nd_at](int k) constexpr -> int {  // issued after the slot lookup of step k-2
+    int n = 0;
+    if (k - 2 >= -A) n += nd_at(k - 2);
+    if (k - 1 >= -A) n += 1 + nd_at(k - 1);
+    return n + 1;
+  };
+  int sreg[S];
+  auto step = [&](auto K_, int kbase) __attribute__((always_inline)) {
+    constexpr int KC = decltype(K_)::value;  // step index modulo S (steady state) or exact (prologue)
+    const int k = kbase + KC;
+    constexpr int SL = ((KC + A) % S + S) % S;
+    constexpr int DI = ((KC + S - 1) % S + S) % S;
+    sreg[SL] = load_slot(k + A);
+    if (k + S - 1 >= 0) {
+      // wait counts: exact per prologue step, 2 * OPS from step -1 on
+      wait_vm(std::integral_constant<int, wait_at(KC < 0 ? KC : 2)>{});
+      __asm__ volatile("" : "+v"(sreg[DI]));
+      if (k >= 0) barrier();
+      issue(slot_of(k + S - 1, sreg[DI]), DI);
+    }
+    if constexpr (kConvV) {
+      // tile k+1 (issued at step k-2) has landed once at most 2*OPS newer loads remain
+      if (k >= -1) {
+        wait_vm(std::integral_constant<int, 2 * OPS>{});
+        convert_v(((KC + 1) % S + S) % S);
+      }
+    }
+    if (k >= 0 && k < ntiles) compute(k, ((KC % S) + S) % S);
+  };
+
+  if (ntiles > 0) {
+    // prologue: steps -A .. -1
+    [&]<int... Is>(std::integer_sequence<int, Is...>) __attribute__((always_inline)) {
+      (step(std::integral_constant<int, Is - A>{}, 0), ...);
+    }(std::make_integer_sequence<int, A>{});
+    auto group = [&]<int... Is>(std::integer_sequence<int, Is...>, int n) __attribute__((always_inline)) {
+      (step(std::integral_constant<int, Is>{}, n), ...);
+    };
+    for (int n = 0; n < ntiles; n += S) group(std::make_integer_sequence<int, S>{}, n);
+    wait_vm(std::integral_constant<int, 0>{});  // no DMA may land after the workgroup ends
+  }
+
+  // ---- epilogue: normalise and write this lane's rows ----
+#pragma unroll
+  for (int rb = 0; rb < kXRB; ++rb) {
     float lt = l_run[rb];
     lt += shfl_xor_f(lt, 16);
     lt += shfl_xor_f(lt, 32);
     if (!real[rb]) continue;
-    const int r = r0 + wave * 32 + rb * 16 + c;
+    const int r = r0 + wave * (kXRB * 16) + rb * 16 + c;
     const int t = r / a.group;
     const int g = r - t * a.group;
     const float inv = (lt > 0.f) ? a.v_scale / lt : 0.f;
-    uint16_t* op = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(tok0 + t) * a.out_stride_tok +
-                   (int64_t)(h * a.group + g) * a.out_stride_head;
+    uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) + (int64_t)(tok0 + t) * a.out_stride_tok +
+                             (int64_t)(h * a.group + g) * a.out_stride_head;
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       u32x2 w;
       w[0] = (uint32_t)f2h<QBF16>(o[rb][db][0] * inv) | ((uint32_t)f2h<QBF16>(o[rb][db][1] * inv) << 16);
       w[1] = (uint32_t)f2h<QBF16>(o[rb][db][2] * inv) | ((uint32_t)f2h<QBF16>(o[rb][db][3] * inv) << 16);
-      *reinterpret_cast<u32x2*>(op + db * 16 + 4 * j) = w;
+      *reinterpret_cast<u32x2 MA_GLOBAL*>(op + db * 16 + 4 * j) = w;
     }
   }
 }
@@ -347,9 +410,9 @@ __global__ __launch_bounds__(256) void extend_kernel(const ExtendArgs a) {
 template <bool QBF16>
 static hipError_t launch_extend_q(int kv, dim3 grid, hipStream_t st, const ExtendArgs& a) {
   switch (kv) {
-    case DT_E4M3: hipLaunchKernelGGL((extend_kernel<QBF16, DT_E4M3>), grid, dim3(256), 0, st, a); break;
-    case DT_E5M2: hipLaunchKernelGGL((extend_kernel<QBF16, DT_E5M2>), grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((extend_kernel<QBF16, QBF16 ? DT_BF16 : DT_F16>), grid, dim3(256), 0, st, a);
+    case DT_E4M3: hipLaunchKernelGGL((extend_kernel<QBF16, DT_E4M3>), grid, dim3(kXWaves * 64), 0, st, a); break;
+    case DT_E5M2: hipLaunchKernelGGL((extend_kernel<QBF16, DT_E5M2>), grid, dim3(kXWaves * 64), 0, st, a); break;
+    default: hipLaunchKernelGGL((extend_kernel<QBF16, QBF16 ? DT_BF16 : DT_F16>), grid, dim3(kXWaves * 64), 0, st, a);
   }
   return hipGetLastError();
 }
