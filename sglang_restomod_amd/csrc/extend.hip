@@ -11,7 +11,8 @@
 // heads that share a kv head are served from one copy of each K/V tile in LDS. Row tiles
 // are launched heaviest-first (the last tokens of a causal sequence see the most keys).
 //
-// Per 64-key tile, per wave, MFMA 16x16x32 with fp32 accumulate:
+// Per 64-key tile, per wave (scores of all 64 keys, then one online-softmax update, then
+// PV), MFMA 16x16x32 with fp32 accumulate:
 //   S^T[key, row] = K[key, :] . Q[row, :]     A = K from LDS, B = Q^T (registers, whole kernel)
 //   O^T[d, row] += V^T[d, key] P^T[key, row]  A = V^T read transposed from LDS
 //                                             (ds_read_b64_tr_b16 / _tr_b8), B = P^T straight
@@ -219,93 +220,93 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   const int vrow = (4 * j + (c >> 2)) * kRowB + ((lane & 3) >> 1) * 16 + (lane & 1) * 8;
   const int vs1 = (4 * j + (c >> 2)) & 7;
 
-  // ---- one tile, as two 32-key halves (scores, softmax and PV per half) ----
+  // ---- one tile: scores for all 64 keys, one softmax update, PV ----
   auto compute = [&](int tile, int st) __attribute__((always_inline)) {
     const unsigned char* kt = kring[st];
     const unsigned char* vt = vring[st];
+    const int base = key_lo + tile * kXBN;
+    f32x4 s[kXRB][4];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int base = key_lo + tile * kXBN + hf * 32;
-      // S^T = K Q^T: key blocks 2hf, 2hf+1 x 4 row blocks
-      f32x4 s[kXRB][2];
+    for (int rb = 0; rb < kXRB; ++rb)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) s[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (kFp8) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const u32x4 raw = *reinterpret_cast<const u32x4*>(kt + (kb * 2 + hh) * 1024 + lane * 16);
+          u32x4 k0, k1;
+          cvt16_fp8<KV, QBF16>(raw, k0, k1);
+#pragma unroll
+          for (int rb = 0; rb < kXRB; ++rb) {
+            s[rb][kb] = mfma16t<QBF16>(k0, qv[rb][2 * hh], s[rb][kb]);
+            s[rb][kb] = mfma16t<QBF16>(k1, qv[rb][2 * hh + 1], s[rb][kb]);
+          }
+        }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(kt + (kb * 4 + kk) * 1024 + lane * 16);
+#pragma unroll
+          for (int rb = 0; rb < kXRB; ++rb) s[rb][kb] = mfma16t<QBF16>(kf, qv[rb][kk], s[rb][kb]);
+        }
+    }
+    const bool full = (base >= full_lo) && (base + kXBN <= full_hi);
+    u32x4 pk[kXRB][2];
+    float alpha[kXRB];
+    bool grew = false;
+#pragma unroll
+    for (int rb = 0; rb < kXRB; ++rb) {
+      if (!full) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int pos = base + kb * 16 + 4 * j + i;
+            if (pos < lo_r[rb] || pos >= hi_r[rb]) s[rb][kb][i] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        mx = fmaxf(mx, fmaxf(fmaxf(s[rb][kb][0], s[rb][kb][1]), fmaxf(s[rb][kb][2], s[rb][kb][3])));
+      alpha[rb] = 1.f;
+      if (__builtin_amdgcn_ballot_w64(mx > m_run[rb])) {
+        mx = fmaxf(mx, shfl_xor_f(mx, 16));
+        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        const float m_new = fmaxf(m_run[rb], mx);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        grew |= (m_new != m_run[rb]);
+        alpha[rb] = __builtin_amdgcn_exp2f((m_run[rb] - m_use) * a.scale_log2);
+        m_run[rb] = m_new;
+      }
+      const float m_use = (m_run[rb] == -INFINITY) ? 0.f : m_run[rb];
+      const float msc = m_use * a.scale_log2;
+      float p[16];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[kb * 4 + i] = __builtin_amdgcn_exp2f(s[rb][kb][i] * a.scale_log2 - msc);
+      float ps = 0.f;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) ps += p[x];
+      l_run[rb] = l_run[rb] * alpha[rb] + ps;
+#pragma unroll
+      for (int st2 = 0; st2 < 2; ++st2)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pk[rb][st2][w] = pack_f16(p[8 * st2 + 2 * w], p[8 * st2 + 2 * w + 1]);
+    }
+    if (__builtin_amdgcn_ballot_w64(grew)) {
 #pragma unroll
       for (int rb = 0; rb < kXRB; ++rb)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) s[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (kFp8) {
+        for (int db = 0; db < 8; ++db) o[rb][db] *= alpha[rb];
+    }
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            const u32x4 raw = *reinterpret_cast<const u32x4*>(kt + ((2 * hf + kb) * 2 + hh) * 1024 + lane * 16);
-            u32x4 k0, k1;
-            cvt16_fp8<KV, QBF16>(raw, k0, k1);
-#pragma unroll
-            for (int rb = 0; rb < kXRB; ++rb) {
-              s[rb][kb] = mfma16t<QBF16>(k0, qv[rb][2 * hh], s[rb][kb]);
-              s[rb][kb] = mfma16t<QBF16>(k1, qv[rb][2 * hh + 1], s[rb][kb]);
-            }
-          }
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            const u32x4 kf = *reinterpret_cast<const u32x4*>(kt + ((2 * hf + kb) * 4 + kk) * 1024 + lane * 16);
-#pragma unroll
-            for (int rb = 0; rb < kXRB; ++rb) s[rb][kb] = mfma16t<QBF16>(kf, qv[rb][kk], s[rb][kb]);
-          }
-      }
-      // online softmax per row (lane column)
-      const bool full = (base >= full_lo) && (base + 32 <= full_hi);
-      u32x4 pk[kXRB];
-      float alpha[kXRB];
-      bool grew = false;
-#pragma unroll
-      for (int rb = 0; rb < kXRB; ++rb) {
-        if (!full) {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int pos = base + kb * 16 + 4 * j + i;
-              if (pos < lo_r[rb] || pos >= hi_r[rb]) s[rb][kb][i] = -INFINITY;
-            }
-        }
-        float mx = fmaxf(fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), fmaxf(s[rb][0][2], s[rb][0][3])),
-                         fmaxf(fmaxf(s[rb][1][0], s[rb][1][1]), fmaxf(s[rb][1][2], s[rb][1][3])));
-        // the row maximum only changes if some lane holds a score above it: then (and
-        // only then) reduce across the four lanes of each row
-        alpha[rb] = 1.f;
-        if (__builtin_amdgcn_ballot_w64(mx > m_run[rb])) {
-          mx = fmaxf(mx, shfl_xor_f(mx, 16));
-          mx = fmaxf(mx, shfl_xor_f(mx, 32));
-          const float m_new = fmaxf(m_run[rb], mx);
-          const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-          grew |= (m_new != m_run[rb]);
-          alpha[rb] = __builtin_amdgcn_exp2f((m_run[rb] - m_use) * a.scale_log2);
-          m_run[rb] = m_new;
-        }
-        const float m_use = (m_run[rb] == -INFINITY) ? 0.f : m_run[rb];
-        const float msc = m_use * a.scale_log2;
-        float p[8];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) p[kb * 4 + i] = __builtin_amdgcn_exp2f(s[rb][kb][i] * a.scale_log2 - msc);
-        const float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-        l_run[rb] = l_run[rb] * alpha[rb] + ps;
-        // P^T operand: keys of block 2hf (4j+i), then of block 2hf+1 (16+4j+i)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) pk[rb][w] = pack_f16(p[2 * w], p[2 * w + 1]);
-      }
-      if (__builtin_amdgcn_ballot_w64(grew)) {
-#pragma unroll
-        for (int rb = 0; rb < kXRB; ++rb)
-#pragma unroll
-          for (int db = 0; db < 8; ++db) o[rb][db] *= alpha[rb];
-      }
-      // O^T += V^T P^T: 8 head-dim blocks x 4 row blocks
+    for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         u32x4 va;
@@ -317,8 +318,6 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
               (__attribute__((address_space(3))) i32x2*)(ptr)));
           va = cvt8_fp8<KV, false>(raw[0], raw[1]);
         } else {
-          // row t = hf*32 + 16*half + 4j + e; its swizzle is lane-constant (t & 7 = vs1), so
-          // chunk (2db + cc/2) ^ swz(t) = 2 (db ^ vs1) + cc/2
           const unsigned char* pcol = vt + vrow + ((db ^ vs1) << 5);
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
@@ -330,9 +329,8 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
           }
         }
 #pragma unroll
-        for (int rb = 0; rb < kXRB; ++rb) o[rb][db] = mfma16t<false>(va, pk[rb], o[rb][db]);
+        for (int rb = 0; rb < kXRB; ++rb) o[rb][db] = mfma16t<false>(va, pk[rb][hf], o[rb][db]);
       }
-    }
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   };
 

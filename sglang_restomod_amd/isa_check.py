@@ -1,58 +1,134 @@
-"""Static check of the generated gfx950 assembly for in-flight register hazards.
+"""Static checks of the generated gfx950 assembly.
 
-Kernels that issue their loads as inline assembly and wait with explicit
-``s_waitcnt vmcnt(N)`` rely on nothing touching a load's destination registers
-until a wait has retired it. This script simulates the in-order vector-memory
-counter over each kernel's instruction list (twice back to back, so that loads
-pending at the end of a loop body meet the loop top) and reports every read or
-write of a destination register whose load is still outstanding.
+In-flight register hazards: kernels that issue their loads as inline assembly
+and wait with explicit ``s_waitcnt vmcnt(N)`` rely on nothing touching a load's
+destination registers until a wait has retired it. ``check`` runs a forward
+dataflow over each kernel's control-flow graph (basic blocks split at labels and
+branches): the state maps every possibly outstanding load to the smallest number
+of vector-memory instructions issued after it on any path, a wait ``vmcnt(N)``
+retires the loads with at least N younger instructions (completion is in order),
+paths merge by union with the minimum count, and a load with 63 younger
+instructions has necessarily completed. Any instruction that reads or writes a
+destination register of a possibly outstanding load is reported.
 
     python -m sglang_restomod_amd.isa_check file.s   (exit status 1 on any hazard)
 """
-import re, sys
+import re
+import sys
+
+VMEM = ('global_load', 'global_store', 'global_atomic', 'buffer_', 'flat_', 'scratch_')
+LOADS = ('global_load', 'buffer_load', 'flat_load', 'scratch_load')
+
 
 def regs(tok):
     tok = tok.strip().rstrip(',')
     m = re.match(r'([va])\[(\d+):(\d+)\]', tok)
-    if m: return {f"{m.group(1)}{i}" for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+    if m:
+        return {f"{m.group(1)}{i}" for i in range(int(m.group(2)), int(m.group(3)) + 1)}
     m = re.match(r'([va])(\d+)$', tok)
-    if m: return {tok}
+    if m:
+        return {tok}
     return set()
 
-def check(body, name):
-    """Simulate the vector-memory counter over `body`; return the hazard count."""
-    pending = []  # list of (seq, dst_regs, text)
-    issued = 0
-    problems = 0
-    for ln, line in enumerate(body):
-        t = line.strip()
-        if not t or t.startswith(('.', ';')) or t.endswith(':'): continue
-        op = t.split()[0]
-        m = re.match(r's_waitcnt\s+vmcnt\((\d+)\)', t)
-        if m:
-            n = int(m.group(1))
-            # in-order: all but the last n outstanding ops retire
-            if len(pending) > n: pending = pending[len(pending) - n:] if n else []
+
+def _parse(body):
+    """Instructions (text) and label -> instruction index."""
+    insts, labels = [], {}
+    for line in body:
+        t = line.split(';')[0].strip()
+        if not t:
             continue
-        if op.startswith(('s_endpgm', 's_branch', 's_cbranch', 's_setpc')):
+        if t.endswith(':'):
+            labels[t[:-1]] = len(insts)
             continue
-        args = t[len(op):].split(',')
-        is_vm = op.startswith(('global_load', 'global_store', 'buffer_', 'flat_', 'scratch_', 'global_atomic'))
-        # uses: all register operands of this instruction
-        used = set()
-        for a in args: used |= regs(a.split()[0] if a.split() else a)
-        for (seq, dst, txt) in pending:
-            if dst & used:
-                problems += 1
-                if problems <= 10:
-                    print(f"{name}: line {ln}: '{t}' touches {sorted(dst & used)} of in-flight '{txt}'")
-        if is_vm:
-            dst = set()
-            if op.startswith(('global_load', 'buffer_load', 'flat_load', 'scratch_load')) and 'lds' not in op:
-                dst = regs(args[0])
-            pending.append((issued, dst, t))
-            issued += 1
-    return problems
+        if t.startswith('.'):
+            continue
+        insts.append(t)
+    return insts, labels
+
+
+def _blocks(insts, labels):
+    """Basic blocks as (start, end) index pairs and their successor block indices."""
+    leaders = {0} | set(labels.values())
+    for i, t in enumerate(insts):
+        if t.startswith(('s_branch', 's_cbranch', 's_endpgm', 's_setpc')):
+            leaders.add(i + 1)
+    starts = sorted(x for x in leaders if x < len(insts))
+    index = {s: k for k, s in enumerate(starts)}
+    blocks, succ = [], []
+    for k, s0 in enumerate(starts):
+        e = starts[k + 1] if k + 1 < len(starts) else len(insts)
+        blocks.append((s0, e))
+        last = insts[e - 1]
+        op = last.split()[0]
+        nxt = [index[e]] if e in index else []
+        if op == 's_branch':
+            succ.append([index[labels[last.split()[1]]]])
+        elif op.startswith('s_cbranch'):
+            succ.append([index[labels[last.split()[1]]]] + nxt)
+        elif op.startswith(('s_endpgm', 's_setpc')):
+            succ.append([])
+        else:
+            succ.append(nxt)
+    return blocks, succ
+
+
+def _step(state, t, hazards, idx):
+    """Apply instruction `t` (index idx) to `state` {load_idx: (younger, dst, text)}."""
+    m = re.search(r'vmcnt\((\d+)\)', t) if t.startswith('s_waitcnt') else None
+    if m:
+        n = int(m.group(1))
+        return {k: v for k, v in state.items() if v[0] < n}
+    op = t.split()[0]
+    args = t[len(op):].split(',')
+    used = set()
+    for a in args:
+        used |= regs(a.split()[0] if a.split() else a)
+    for k, (younger, dst, txt) in state.items():
+        if dst & used:
+            hazards.add((idx, k, f"'{t}' touches {sorted(dst & used)} of in-flight '{txt}'"))
+    if op.startswith(VMEM):
+        state = {k: (v[0] + 1, v[1], v[2]) for k, v in state.items() if v[0] + 1 < 63}
+        if op.startswith(LOADS) and 'lds' not in op:
+            state[idx] = (0, regs(args[0]), t)
+    return state
+
+
+def _merge(a, b):
+    out = dict(a)
+    for k, v in b.items():
+        out[k] = v if k not in out else (min(out[k][0], v[0]), v[1], v[2])
+    return out
+
+
+def check(body, name, verbose=True):
+    """Dataflow over the kernel's blocks; return the number of distinct hazards."""
+    insts, labels = _parse(body)
+    if not insts:
+        return 0
+    blocks, succ = _blocks(insts, labels)
+    ins = [None] * len(blocks)
+    ins[0] = {}
+    work = [0]
+    hazards = set()
+    while work:
+        b = work.pop()
+        state = ins[b]
+        s0, e = blocks[b]
+        for i in range(s0, e):
+            state = _step(state, insts[i], hazards, i)
+        for nb in succ[b]:
+            merged = state if ins[nb] is None else _merge(ins[nb], state)
+            if ins[nb] is None or merged != ins[nb]:
+                ins[nb] = merged
+                if nb not in work:
+                    work.append(nb)
+    if verbose:
+        for i, (idx, k, msg) in enumerate(sorted(hazards)):
+            if i >= 10:
+                break
+            print(f"{name}: instruction {idx}: {msg}")
+    return len(hazards)
 
 # Writes through the scalar data cache (scalar stores and atomics, and that cache's
 # write-back / discard) must never appear in this library's kernels.
@@ -69,11 +145,11 @@ def check_file(path, verbose=False):
     """Return the number of hazards over all kernels of an assembly listing."""
     s = open(path).read()
     total = 0
-    for name in re.findall(r"^(_ZN2ma\w*(?:partial|extend)\w*):", s, re.M):
+    for name in re.findall(r"^(_ZN2ma\w*):", s, re.M):
         start = s.index(name + ":")
         end = s.index(".Lfunc_end", start)
-        lines = s[start:end].splitlines()
-        p = check(lines + lines, name[:50])
+        lines = s[start:end].splitlines()[1:]
+        p = check(lines, name[:50])
         if verbose:
             print(f"{name[:60]}: {p} hazards")
         total += p

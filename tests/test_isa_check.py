@@ -29,8 +29,29 @@ def test_register_read_after_its_wait_is_clean(tmp_path):
 def test_in_order_counting_keeps_later_loads_in_flight(tmp_path):
     body = ("\tglobal_load_dwordx4 a[0:3], v[2:3], off\n\tglobal_load_dwordx4 a[4:7], v[2:3], off\n"
             "\ts_waitcnt vmcnt(1)\n\tv_mov_b32 v9, a1\n\tv_mov_b32 v10, a5\n\ts_waitcnt vmcnt(0)\n")
-    # only the read of a5 is a hazard; the body is simulated twice (loop wrap-around)
+    # only the read of a5 is a hazard
+    assert isa_check.check_file(_write(tmp_path, body)) == 1
+
+
+def test_load_pending_across_a_loop_back_edge_is_a_hazard(tmp_path):
+    # the next iteration reads a1, and reloads a[0:3], before waiting for the previous load
+    body = (".LBB0_1:\n\tv_mov_b32 v9, a1\n\tglobal_load_dwordx4 a[0:3], v[2:3], off\n"
+            "\ts_cbranch_scc1 .LBB0_1\n\ts_waitcnt vmcnt(0)\n\ts_endpgm\n")
     assert isa_check.check_file(_write(tmp_path, body)) == 2
+
+
+def test_wait_at_the_loop_top_retires_the_load(tmp_path):
+    body = (".LBB0_1:\n\ts_waitcnt vmcnt(0)\n\tv_mov_b32 v9, a1\n\tglobal_load_dwordx4 a[0:3], v[2:3], off\n"
+            "\ts_cbranch_scc1 .LBB0_1\n\ts_waitcnt vmcnt(0)\n\ts_endpgm\n")
+    assert isa_check.check_file(_write(tmp_path, body)) == 0
+
+
+def test_out_of_line_block_is_checked_in_execution_order(tmp_path):
+    # .LBB0_2 is laid out after the load but runs before it: no hazard
+    body = ("\ts_cbranch_scc1 .LBB0_2\n.LBB0_1:\n\tglobal_load_dword v7, v[2:3], off\n"
+            "\ts_waitcnt vmcnt(0)\n\tv_mov_b32 v9, v7\n\ts_endpgm\n"
+            ".LBB0_2:\n\tv_mov_b32 v7, 1.0\n\ts_branch .LBB0_1\n")
+    assert isa_check.check_file(_write(tmp_path, body)) == 0
 
 
 def test_scalar_cache_writes_are_found(tmp_path):
