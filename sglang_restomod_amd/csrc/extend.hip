@@ -23,8 +23,8 @@
 // softmax state fp32.
 //
 // Memory pipeline: K and V tiles travel HBM -> LDS by DMA (global_load_lds) into an
-// S-stage ring, with S-1 tiles in flight while one computes; each wave moves an eighth
-// of every tile. K lands as MFMA fragment blocks (block (kb, kk) = 16 keys x 8 head-dim
+// S-stage ring (5 stages for 16-bit KV, 8 for fp8), with S-1 tiles in flight while one
+// computes; each wave moves an eighth of every tile. K lands as MFMA fragment blocks (block (kb, kk) = 16 keys x 8 head-dim
 // entries, lane l's 16 bytes at l * 16), so each operand read is one conflict-free
 // ds_read_b128; V lands row-major with an XOR swizzle of its 16-byte chunks. Slots are
 // looked up S+1 tiles ahead. The loads are inline assembly with explicit wait counts,
@@ -79,9 +79,13 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   constexpr int kVBlk = kStageB / 1024 / kXWaves;  // V DMA blocks per wave per tile
   constexpr int ND = kKBlk + kVBlk;              // DMA instructions per wave per tile
   constexpr int OPS = 1 + ND;                    // plus one slot lookup
-  constexpr int S = 4;                           // pipeline stages
+  // pipeline stages: 5 x 32 KB for 16-bit KV (all 160 KB of LDS), 8 x 16 KB for fp8
+  constexpr int S = kFp8 ? 8 : 5;
   constexpr int A = S + 1;                       // slot lookahead (tiles)
   static_assert((S - 1) * ND + 2 <= 63, "outstanding loads exceed the counter");
+  // the wait before a tile's barrier counts on its loads preceding the slot lookup of
+  // step k-2 (tile k is issued at step k-S+1 <= k-3)
+  static_assert(S >= 4, "the schedule needs at least four stages");
   static_assert(kKBlk >= 1 && kKSub % kKBlk == 0, "a wave's K blocks share one key block");
 
   __shared__ __attribute__((aligned(1024))) unsigned char kring[S][kStageB];
@@ -361,9 +365,10 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       issue(slot_of(k + S - 1, sreg[DI]), DI);
     }
     if constexpr (kConvV) {
-      // tile k+1 (issued at step k-2) has landed once at most 2*OPS newer loads remain
+      // tile k+1 (issued at step k+2-S) has landed once at most (S-2)*OPS newer
+      // instructions (those of steps k+3-S .. k) remain
       if (k >= -1) {
-        wait_vm(std::integral_constant<int, 2 * OPS>{});
+        wait_vm(std::integral_constant<int, (S - 2) * OPS>{});
         convert_v(((KC + 1) % S + S) % S);
       }
     }
