@@ -10,7 +10,8 @@ resident in HBM:
   slots. ``value`` = algorithmic GB/s (K+V once per token and kv head, 4 B of
   slot index per token, q in and out) over the timed region.
 * ``--secondary`` adds the other workloads (extend TFLOP/s, fp8 decode GB/s,
-  verify GB/s) as extra fields of the same JSON line.
+  verify GB/s, and the KV write of an extend batch into an fp8 pool) as extra fields
+  of the same JSON line.
 
 ``value`` is whole-job throughput: algorithmic bytes of the K timed steps over
 the wall time between the two synchronisations. ``roofline`` compares the
@@ -181,6 +182,36 @@ def _cpu_baseline(w, budget_s):
     return med, frac, cores, rows
 
 
+def _measure_kv_write(steps, warmup):
+    """The pool write of an extend batch: the extend workload's new tokens (11,179 x 8 kv
+    heads x 128, bf16 K and V) quantized into an e4m3 pool at shuffled slots."""
+    import torch
+
+    from sglang_restomod_amd import workloads
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    spec = workloads.WORKLOADS[2]
+    gen = torch.Generator().manual_seed(2)
+    T = int(workloads.make(2, device=torch.device("cpu")).extend_lens.sum())
+    H, D = spec["heads_kv"], spec["dim"]
+    dev = torch.device("cuda:0")
+    k = torch.randn(T, H, D, generator=gen).to(torch.bfloat16).to(dev)
+    v = torch.randn(T, H, D, generator=gen).to(torch.bfloat16).to(dev)
+    slots = 4 * T
+    loc = torch.randperm(slots, generator=gen)[:T].to(dev)
+    kc = torch.zeros(slots, H, D, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    vc = torch.zeros_like(kc)
+    fn = lambda: ops.set_kv_buffer(kc, vc, loc, k, v, 0.9, 1.1)
+    wall_ms, per = _time_gpu(fn, steps, warmup)
+    nbytes = 2 * T * H * D * (2 + 1) + 8 * T
+    ev = statistics.mean(per)
+    return {"workload": f"kv_write_t{T}_h{H}_d{D}_bf16_to_e4m3", "mode": "kv_write",
+            "ms_per_step": round(wall_ms, 5), "event_ms_mean": round(ev, 5),
+            "GBps": round(nbytes / (ev * 1e-3) / 1e9, 2),
+            "hbm_frac": round(nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": nbytes}
+
+
 def _workload_metrics(w):
     from sglang_restomod_amd import workloads
 
@@ -285,6 +316,7 @@ def main():
         }
     if args.secondary:
         sec = {}
+        sec["kv_write"] = _measure_kv_write(max(10, args.steps // 2), args.warmup)
         for idx, fmt in ((0, None), (2, None), (3, "e4m3"), (3, "e5m2"), (4, None)):
             if idx == args.workload:
                 continue

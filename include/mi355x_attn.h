@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 3
+#define MA_ABI_VERSION 4
 
 /* dtype codes */
 #define MA_DT_F16 0
@@ -145,6 +145,25 @@ int ma_paged_extend(const void* q, int64_t q_stride_tok, int64_t q_stride_head, 
                     int num_kv_heads, int head_dim, int causal, int sliding_window,
                     float softmax_scale, float k_scale, float v_scale, void* out,
                     int64_t out_stride_tok, int64_t out_stride_head, void* stream);
+
+/*
+ * KV write into the token pools with quantisation on write.
+ * Replaces the pool write before every attention call (set_kv_buffer, called at
+ * flash_attn_v100_backend.py:1174-1182 and 1038-1046, draft_decode.py:132-139) with
+ * SGLang's token-pool semantics: row t of k and v ([num_tokens, num_kv_heads, head_dim],
+ * src_dtype MA_DT_F16 / MA_DT_BF16, any token/head stride, head_dim contiguous and a
+ * power of two in 8..2048) is stored at pool slot loc[t] of k_cache / v_cache.
+ *   cache_dtype = src_dtype: a copy (scales ignored).
+ *   otherwise: if apply_scale, x / scale in fp32 rounded to src_dtype, then cast to the
+ *     cache dtype (fp8: round to nearest even; past the largest finite value e4m3fn
+ *     gives NaN, e5m2 infinity).
+ * Slots outside [0, num_slots) are skipped. Slots must be distinct.
+ */
+int ma_set_kv_buffer(const void* k, const void* v, int64_t src_stride_tok, int64_t src_stride_head,
+                     int src_dtype, const int64_t* loc, int64_t num_tokens, int num_kv_heads,
+                     int head_dim, void* k_cache, void* v_cache, int64_t cache_stride_row,
+                     int64_t cache_stride_head, int cache_dtype, int64_t num_slots, float k_scale,
+                     float v_scale, int apply_scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -50,6 +50,12 @@ SIGNATURES = {
         c_float, c_float, c_float, c_void_p, c_size_t,  # scales, workspace, bytes
         c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
     ]),
+    "ma_set_kv_buffer": (c_int, [
+        c_void_p, c_void_p, c_int64, c_int64, c_int,  # k, v, strides, source dtype
+        c_void_p, c_int64, c_int, c_int,              # loc, num_tokens, hkv, dim
+        c_void_p, c_void_p, c_int64, c_int64, c_int,  # caches, strides, cache dtype
+        c_int64, c_float, c_float, c_int, c_void_p,   # num_slots, scales, apply, stream
+    ]),
     "ma_paged_extend": (c_int, [
         c_void_p, c_int64, c_int64, c_int, c_int64,   # q, strides, dtype, num_tokens
         c_void_p, c_void_p, c_int64, c_int64, c_int,  # k, v, strides, kv dtype

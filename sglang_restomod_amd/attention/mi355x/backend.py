@@ -33,6 +33,7 @@ from typing import Optional
 import torch
 
 from . import ops
+from .backend_registry import env_flag
 from .draft_decode_plan import layer_shape_reason
 from .masks import resolve_layer_mask
 
@@ -47,6 +48,9 @@ FP8_KV = (torch.float8_e4m3fn, torch.float8_e5m2)
 MODE_DECODE = "decode"
 MODE_EXTEND = "extend"
 MODE_VERIFY = "verify"
+# write new K/V with this library's kernel into the pool's buffers instead of calling the
+# pool's own set_kv_buffer (same stored bytes; see ops.set_kv_buffer)
+ENV_NATIVE_KV_WRITE = "SGLANG_MI355X_NATIVE_KV_WRITE"
 
 
 @dataclass
@@ -110,6 +114,7 @@ class MI355XAttnBackend(_EngineBase):
         if self.req_to_token.dtype != torch.int32:
             raise ValueError("req_to_token must be int32")
         self.head_dim = head_dim
+        self.native_kv_write = env_flag(ENV_NATIVE_KV_WRITE, "0")
         self.forward_metadata: Optional[MI355XForwardMetadata] = None
         self._workspace: Optional[torch.Tensor] = None
         # graph buffers (init_cuda_graph_state)
@@ -355,7 +360,14 @@ class MI355XAttnBackend(_EngineBase):
     def _save_kv(self, layer, loc, k, v) -> None:
         if k is None:
             return
-        self.token_to_kv_pool.set_kv_buffer(layer, loc, k, v, layer.k_scale, layer.v_scale)
+        if not self.native_kv_write:
+            self.token_to_kv_pool.set_kv_buffer(layer, loc, k, v, layer.k_scale, layer.v_scale)
+            return
+        k_cache, v_cache = self._caches(layer)
+        ks = float(layer.k_scale_float) if getattr(layer, "k_scale", None) is not None else None
+        vs = float(layer.v_scale_float) if getattr(layer, "v_scale", None) is not None else None
+        hkv, d = int(layer.tp_k_head_num), int(layer.head_dim)
+        ops.set_kv_buffer(k_cache, v_cache, loc, k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), ks, vs)
 
     def forward_decode(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True, **kwargs):
         self._check_layer(layer, kwargs)

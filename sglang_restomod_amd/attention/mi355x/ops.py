@@ -2,6 +2,7 @@
 
 * ``grouped_decode_forward`` - sglang_restomod/attention/v100/tilelang/_paged_adapter.py:402-486
 * ``paged_forward``          - _paged_adapter.py:567-759 (extend, and the linear-verify branch)
+* ``set_kv_buffer``          - the token pool's write called at flash_attn_v100_backend.py:1174-1182
 
 Shapes and dtypes are validated here and raise ``ValueError`` the way the
 reference's gates do (_paged_adapter.py:417-418, 538-541). Workspaces are
@@ -397,3 +398,48 @@ def paged_extend_forward(
     )
     _lib.check(status, "ma_paged_extend")
     return out
+
+
+def set_kv_buffer(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    loc: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_scale: Optional[float] = None,
+    v_scale: Optional[float] = None,
+) -> None:
+    """Store new K/V rows ``k``/``v`` [T, Hkv, D] at pool slots ``loc`` [T] (the token
+    pool's ``set_kv_buffer``): a copy into a pool of the source dtype; otherwise, with
+    scales given, ``x / scale`` rounded to the source dtype, then cast to the pool dtype
+    (fp8: round to nearest even, e4m3fn overflow -> NaN, e5m2 overflow -> inf).
+    Pools are [slots, Hkv, D] (or the paged view); slots outside the pool are skipped.
+    """
+    if k.dim() == 2:
+        k = k.view(k.shape[0], -1, k_cache.shape[-1])
+        v = v.view(v.shape[0], -1, v_cache.shape[-1])
+    if k.shape != v.shape or k.dim() != 3:
+        raise ValueError("k and v must be [tokens, kv_heads, head_dim] of one shape")
+    if k.dtype != v.dtype or k_cache.dtype != v_cache.dtype:
+        raise ValueError("k/v and the two caches must share their dtypes")
+    dev = _check_device(k, v, k_cache, v_cache, loc)
+    T, H, D = k.shape
+    row, head, ps, Hc, Dc = kv_layout(k_cache)
+    if kv_layout(v_cache)[:2] != (row, head):
+        raise ValueError("K and V caches must share one layout")
+    if (Hc, Dc) != (H, D):
+        raise ValueError(f"cache heads/dim {(Hc, Dc)} do not match the rows {(H, D)}")
+    if k.stride() != v.stride() or k.stride(-1) != 1:
+        k, v = k.contiguous(), v.contiguous()
+    slots = k_cache.shape[0] * (ps if k_cache.dim() == 4 else 1)
+    loc64 = loc.to(torch.int64).contiguous()
+    apply = k_cache.dtype != k.dtype and k_scale is not None
+    ks = float(k_scale) if apply else 1.0
+    vs = float(v_scale) if (apply and v_scale is not None) else (1.0 if not apply else ks)
+    status = _lib.load().ma_set_kv_buffer(
+        k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), q_dtype_code(k.dtype),
+        loc64.data_ptr(), T, H, D,
+        k_cache.data_ptr(), v_cache.data_ptr(), row, head, kv_dtype_code(k_cache.dtype),
+        slots, ks, vs, 1 if apply else 0, _stream_ptr(dev),
+    )
+    _lib.check(status, "ma_set_kv_buffer")

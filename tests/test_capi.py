@@ -87,3 +87,29 @@ def test_workspace_size_formula(lib):
     n = lib.ma_splitkv_workspace_bytes(256, 128)
     # two partial pieces of up to 32 rows per wave, 4 waves per workgroup
     assert n >= 256 * 4 * 2 * 32 * 129 * 4 and n % 256 == 0
+
+
+def _kvw_args(**over):
+    args = dict(k=1 << 20, v=1 << 21, sst=1024, ssh=128, sdt=1, loc=1 << 22, T=4, hkv=8, dim=128,
+                kc=1 << 23, vc=1 << 24, crs=1024, chs=128, cdt=2, slots=100, ks=1.0, vs=1.0, apply=1,
+                stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("over,msg", [
+    ({"sdt": 2}, "source dtype"),
+    ({"cdt": 7}, "cache dtype"),
+    ({"dim": 100}, "power of two"),
+    ({"ks": 0.0}, "positive"),
+    ({"k": (1 << 20) + 4}, "aligned"),
+    ({"sst": 1001}, "source strides"),
+    ({"hkv": 0}, "bad sizes"),
+])
+def test_kv_write_rejects_bad_arguments(lib, over, msg):
+    assert lib.ma_set_kv_buffer(*_kvw_args(**over)) != 0
+    assert msg in lib.ma_last_error().decode()
+
+
+def test_kv_write_of_nothing_is_a_no_op(lib):
+    assert lib.ma_set_kv_buffer(*_kvw_args(T=0)) == 0

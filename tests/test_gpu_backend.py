@@ -173,3 +173,34 @@ def test_decode_in_a_hip_graph_replays_with_new_lengths():
         ref = oracle.decode(to_f64(q_static).reshape(bs, HQ, D), kp, vp, eng.req_to_token.cpu().numpy(), rows,
                             fb.seq_lens.tolist(), softmax_scale=layer.scaling)
         assert_attn_close(got.reshape(bs, HQ, D), ref, what=f"graph replay {step}")
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float8_e5m2])
+def test_native_kv_write_matches_the_pool_write(kv_dtype, monkeypatch):
+    """The library's KV write leaves the pool byte-identical to the pool's own write."""
+    engines, outs = [], []
+    for native in (False, True):
+        monkeypatch.setenv("SGLANG_MI355X_NATIVE_KV_WRITE", "1" if native else "0")
+        gen = torch.Generator().manual_seed(21)
+        eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=kv_dtype, pool_size=4000, max_reqs=4, context_len=2048)
+        layer = _layer(kv_dtype)
+        be = _backend(eng)
+        assert be.native_kv_write == native
+        fb = eng.batch("EXTEND", [0, 1], new_tokens=[150, 40])
+        q, k, v = _rand(gen, 190, HQ * D), _rand(gen, 190, HKV, D), _rand(gen, 190, HKV, D)
+        be.init_forward_metadata(fb)
+        o1 = be.forward_extend(q, k, v, layer, fb)
+        fb = eng.batch("DECODE", [1, 0], new_tokens=[1, 1])
+        q, k, v = _rand(gen, 2, HQ * D), _rand(gen, 2, HKV, D), _rand(gen, 2, HKV, D)
+        be.init_forward_metadata(fb)
+        o2 = be.forward_decode(q, k, v, layer, fb)
+        torch.cuda.synchronize()
+        engines.append(eng)
+        outs.append((o1, o2))
+    for name in ("k_buffer", "v_buffer"):
+        a = getattr(engines[0].pool, name)[0]
+        b = getattr(engines[1].pool, name)[0]
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), name
+    assert engines[1].pool.writes == 0 and engines[0].pool.writes == 2
+    for x, y in zip(outs[0], outs[1]):
+        assert torch.equal(x, y)
