@@ -299,7 +299,7 @@ def main():
             "frac": round(head["hbm_frac"] if bound_hbm else head["mfma_frac"], 4),
             "traffic": _traffic(kernel, head["workload"]),
             "kernel_ms": round(head["event_ms_mean"], 5),
-            "timing": ("HIP events on the launch stream around each call (split-KV partial + combine)"
+            "timing": ("HIP events on the launch stream around each call (split-KV partial + merge)"
                        if bound_hbm else "HIP events on the launch stream around each call"),
         },
     }
