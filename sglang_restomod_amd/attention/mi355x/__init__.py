@@ -12,8 +12,11 @@ from __future__ import annotations
 
 
 def register() -> None:
-    """Component entry point: register the backend name(s) and the draft choice."""
+    """Component entry point: register the backend name(s), the draft choice, and the
+    draft factory hook."""
+    from . import draft_backend
     from .backend_registry import install, install_draft_choices
 
     install()
     install_draft_choices()
+    draft_backend.install()
