@@ -8,8 +8,10 @@ branches): the state maps every possibly outstanding load to the smallest number
 of vector-memory instructions issued after it on any path, a wait ``vmcnt(N)``
 retires the loads with at least N younger instructions (completion is in order),
 paths merge by union with the minimum count, and a load with 63 younger
-instructions has necessarily completed. Any instruction that reads or writes a
-destination register of a possibly outstanding load is reported.
+instructions has necessarily completed. Any instruction that reads, or writes
+other than as a later load's destination, a destination register of a possibly
+outstanding load is reported (loads return in issue order, so a later load into
+the same register lands after it).
 
     python -m sglang_restomod_amd.isa_check file.s   (exit status 1 on any hazard)
 """
@@ -82,7 +84,10 @@ def _step(state, t, hazards, idx):
     op = t.split()[0]
     args = t[len(op):].split(',')
     used = set()
-    for a in args:
+    is_load = op.startswith(LOADS) and 'lds' not in op
+    for n, a in enumerate(args):
+        if is_load and n == 0:
+            continue  # a later load's destination: loads return in issue order, so its write lands last
         used |= regs(a.split()[0] if a.split() else a)
     for k, (younger, dst, txt) in state.items():
         if dst & used:

@@ -34,10 +34,22 @@ def test_in_order_counting_keeps_later_loads_in_flight(tmp_path):
 
 
 def test_load_pending_across_a_loop_back_edge_is_a_hazard(tmp_path):
-    # the next iteration reads a1, and reloads a[0:3], before waiting for the previous load
+    # the next iteration reads a1 before waiting for the previous iteration's load
     body = (".LBB0_1:\n\tv_mov_b32 v9, a1\n\tglobal_load_dwordx4 a[0:3], v[2:3], off\n"
             "\ts_cbranch_scc1 .LBB0_1\n\ts_waitcnt vmcnt(0)\n\ts_endpgm\n")
-    assert isa_check.check_file(_write(tmp_path, body)) == 2
+    assert isa_check.check_file(_write(tmp_path, body)) == 1
+
+
+def test_a_later_load_into_the_same_register_is_in_order(tmp_path):
+    body = ("\tglobal_load_dwordx4 v[2:5], v[8:9], off\n\tscratch_load_dword v5, off, off offset:4\n"
+            "\ts_waitcnt vmcnt(0)\n\tv_mov_b32 v9, v5\n")
+    assert isa_check.check_file(_write(tmp_path, body)) == 0
+
+
+def test_a_load_whose_address_is_in_flight_is_a_hazard(tmp_path):
+    body = ("\tglobal_load_dwordx2 v[2:3], v[8:9], off\n\tglobal_load_dword v5, v[2:3], off\n"
+            "\ts_waitcnt vmcnt(0)\n")
+    assert isa_check.check_file(_write(tmp_path, body)) == 1
 
 
 def test_wait_at_the_loop_top_retires_the_load(tmp_path):
