@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 4
+#define MA_ABI_VERSION 5
 
 /* dtype codes */
 #define MA_DT_F16 0
@@ -124,27 +124,40 @@ int ma_paged_verify(const void* q, int64_t q_stride_tok, int64_t q_stride_head, 
                     int64_t out_stride_head, void* stream);
 
 /*
+ * Bytes of workspace ma_paged_extend needs for `num_tokens` query tokens in `batch`
+ * sequences: the work list, one 8-byte entry per 256-row tile (at most
+ * ceil(num_tokens * G / 256) + batch, G = num_q_heads / num_kv_heads). 0 for bad
+ * arguments.
+ */
+size_t ma_extend_workspace_bytes(int64_t num_tokens, int num_q_heads, int num_kv_heads, int batch);
+
+/*
  * Prefix-aware paged extend (chunked prefill), MFMA tiles.
  * Replaces the reference's paged extend kernel (_kernels_paged.py:55-393 via
  * get_paged_kernel, _kernels_paged.py:414-436, called from paged_forward,
  * _paged_adapter.py:567-759): query token i of sequence b (tokens
- * query_start_loc[b] .. query_start_loc[b+1]) sees key j < seq_lens[b] with
- * j <= prefix_lens[b] + i when causal, and j >= prefix_lens[b] + i - window when
- * sliding_window >= 0 (a left bound, also for non-causal layers).
+ * query_start_loc[b] .. query_start_loc[b+1], query_start_loc[batch] <= num_tokens)
+ * sees key j < seq_lens[b] with j <= prefix_lens[b] + i when causal, and
+ * j >= prefix_lens[b] + i - window when sliding_window >= 0 (a left bound, also for
+ * non-causal layers).
  *   prefix_lens NULL: seq_lens - query count.
- *   max_q_per_seq: upper bound of query tokens per sequence (grid size).
+ *   batch <= 16384. No host-side maximum of the query lengths is needed: a plan kernel
+ *   lists the row tiles on the device (reference: max_seq_len from seq_lens.max().item(),
+ *   _paged_adapter.py:605-606).
+ *   workspace: ma_extend_workspace_bytes(num_tokens, ...) bytes, 256-byte aligned, no
+ *   initialisation; calls that overlap in time must use different workspaces.
  *   The new tokens' K/V must already be in the pools.
- *   out [num_tokens, num_q_heads, head_dim] in q_dtype. No workspace.
+ *   out [num_tokens, num_q_heads, head_dim] in q_dtype.
  */
 int ma_paged_extend(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
                     int64_t num_tokens, const void* k_cache, const void* v_cache,
                     int64_t kv_stride_row, int64_t kv_stride_head, int kv_dtype,
                     const int32_t* table, int64_t table_stride, const int64_t* row_index,
                     int page_size, const int32_t* seq_lens, const int32_t* query_start_loc,
-                    const int32_t* prefix_lens, int batch, int max_q_per_seq, int num_q_heads,
-                    int num_kv_heads, int head_dim, int causal, int sliding_window,
-                    float softmax_scale, float k_scale, float v_scale, void* out,
-                    int64_t out_stride_tok, int64_t out_stride_head, void* stream);
+                    const int32_t* prefix_lens, int batch, int num_q_heads, int num_kv_heads,
+                    int head_dim, int causal, int sliding_window, float softmax_scale,
+                    float k_scale, float v_scale, void* workspace, size_t workspace_bytes,
+                    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream);
 
 /*
  * KV write into the token pools with quantisation on write.

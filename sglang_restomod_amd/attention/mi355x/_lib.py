@@ -56,13 +56,15 @@ SIGNATURES = {
         c_void_p, c_void_p, c_int64, c_int64, c_int,  # caches, strides, cache dtype
         c_int64, c_float, c_float, c_int, c_void_p,   # num_slots, scales, apply, stream
     ]),
+    "ma_extend_workspace_bytes": (c_size_t, [c_int64, c_int, c_int, c_int]),
     "ma_paged_extend": (c_int, [
         c_void_p, c_int64, c_int64, c_int, c_int64,   # q, strides, dtype, num_tokens
         c_void_p, c_void_p, c_int64, c_int64, c_int,  # k, v, strides, kv dtype
         c_void_p, c_int64, c_void_p, c_int,           # table, stride, row_index, page size
         c_void_p, c_void_p, c_void_p,                 # seq_lens, qsl, prefix
-        c_int, c_int, c_int, c_int, c_int,            # batch, max_q, hq, hkv, dim
+        c_int, c_int, c_int, c_int,                   # batch, hq, hkv, dim
         c_int, c_int, c_float, c_float, c_float,      # causal, window, scales
+        c_void_p, c_size_t,                           # workspace, bytes
         c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
     ]),
 }

@@ -117,6 +117,7 @@ class MI355XAttnBackend(_EngineBase):
         self.native_kv_write = env_flag(ENV_NATIVE_KV_WRITE, "0")
         self.forward_metadata: Optional[MI355XForwardMetadata] = None
         self._workspace: Optional[torch.Tensor] = None
+        self._extend_ws: Optional[torch.Tensor] = None
         # graph buffers (init_cuda_graph_state)
         self._cg_max_bs = 0
         self._cg_row_index: Optional[torch.Tensor] = None
@@ -190,9 +191,9 @@ class MI355XAttnBackend(_EngineBase):
             qsl = torch.zeros(seq.shape[0] + 1, dtype=torch.int32, device=seq.device)
             torch.cumsum(ext, dim=0, dtype=torch.int32, out=qsl[1:])
             md.query_start_loc = qsl
-            if max_q_per_seq is None:
-                max_q_per_seq = int(ext.max().item()) if ext.numel() else 0
-            md.max_q_per_seq = int(max_q_per_seq)
+            # the extend kernel lists its row tiles on the device; only the verifier's
+            # grid needs the longest chain, which callers pass (0: not known)
+            md.max_q_per_seq = int(max_q_per_seq) if max_q_per_seq is not None else 0
         if self._has_swa_pool():
             width = self._max_len(md.seq_lens, seq_lens_cpu if mode == MODE_DECODE else None)
             md.swa_table = self._swa_rows(row_index, max(width, 1))
@@ -221,6 +222,9 @@ class MI355XAttnBackend(_EngineBase):
         max_q = int(max(ext_cpu)) if ext_cpu is not None and len(ext_cpu) else None
         # a draft extend is a few rows over the whole prefix: the verify kernel's shape
         draft = _mode_is(mode, "is_draft_extend_v2") or _mode_is(mode, "is_draft_extend")
+        if draft and max_q is None and forward_batch.extend_seq_lens.numel():
+            # routing needs the longest chain (the reference reads it the same way)
+            max_q = int(forward_batch.extend_seq_lens.max().item())
         md = self.build_metadata(
             MODE_EXTEND, forward_batch.req_pool_indices, forward_batch.seq_lens,
             forward_batch.extend_seq_lens, forward_batch.extend_prefix_lens,
@@ -249,6 +253,22 @@ class MI355XAttnBackend(_EngineBase):
         if self._workspace is None:
             self._workspace = ops.splitkv_workspace(self.device, head_dim=self.head_dim)
         return self._workspace
+
+    def _workspace_for(self, mode: str, num_tokens: int, hq: int, hkv: int, batch: int) -> torch.Tensor:
+        """The split-KV workspace, which also holds an extend call's work list (8 bytes
+        per 256-row tile); a larger buffer only for a batch whose list does not fit."""
+        ws = self.splitkv_workspace()
+        if mode == MODE_VERIFY:
+            return ws
+        need = ops.extend_workspace_bytes(num_tokens, hq, hkv, batch)
+        if ws.numel() >= need:
+            return ws
+        if self._extend_ws is None or self._extend_ws.numel() < need:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"an extend of {num_tokens} tokens needs {need} workspace bytes; "
+                                   "capture smaller batches")
+            self._extend_ws = ops.extend_workspace(self.device, num_tokens, hq, hkv, batch)
+        return self._extend_ws
 
     def init_cuda_graph_state(self, max_bs: int, max_num_tokens: int, kv_indices_buf=None) -> None:
         dev = self.device
@@ -419,8 +439,9 @@ class MI355XAttnBackend(_EngineBase):
                 out=out, block_size=1, num_kv_heads=int(layer.tp_k_head_num),
                 softmax_scale=float(layer.scaling), causal=causal, sliding_window_size=window,
                 linear_verify=md.mode == MODE_VERIFY, k_scale=ks, v_scale=vs, row_index=rows,
-                max_q_len_hint=md.max_q_per_seq,
-                workspace=self.splitkv_workspace() if md.mode == MODE_VERIFY else None)
+                max_q_len_hint=md.max_q_per_seq if md.mode == MODE_VERIFY else None,
+                workspace=self._workspace_for(md.mode, q3.shape[0], hq, int(layer.tp_k_head_num),
+                                              md.seq_lens.shape[0]))
         out = out.reshape(q3.shape[0], hq * d)
         return out if out.dtype == out_dtype else out.to(out_dtype)
 

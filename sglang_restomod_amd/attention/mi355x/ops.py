@@ -114,9 +114,9 @@ def _stream_ptr(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A growable, zero-initialised byte buffer per (device, stream); reuse is ordered by
-    the stream (the split-KV kernels need zeroed counters and leave them zeroed)."""
+def workspace_buffer(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A growable byte buffer per (device, stream), shared by the entry points that take a
+    workspace; calls on one stream are ordered, so they can share it."""
     if nbytes <= 0:
         return None
     key = (str(device), _stream_ptr(device))
@@ -140,10 +140,24 @@ def splitkv_workspace(device: torch.device, num_workgroups: Optional[int] = None
 def _splitkv_ws(lib, dev, nwg: int, D: int, given: Optional[torch.Tensor]):
     nbytes = lib.ma_splitkv_workspace_bytes(nwg, D)
     if given is None:
-        return workspace(dev, nbytes), nbytes
+        return workspace_buffer(dev, nbytes), nbytes
     if given.dtype != torch.uint8 or given.device != dev or given.numel() < nbytes:
         raise ValueError(f"workspace must be a uint8 tensor of at least {nbytes} bytes on {dev}")
     return given, nbytes
+
+
+def extend_workspace_bytes(num_tokens: int, num_q_heads: int, num_kv_heads: int, batch: int) -> int:
+    """Bytes of the work list of an extend call (``ma_extend_workspace_bytes``)."""
+    return int(_lib.load().ma_extend_workspace_bytes(int(num_tokens), int(num_q_heads), int(num_kv_heads),
+                                                      int(batch)))
+
+
+def extend_workspace(device: torch.device, num_tokens: int, num_q_heads: int, num_kv_heads: int,
+                     batch: int) -> torch.Tensor:
+    """A fresh workspace for ``paged_extend_forward`` calls of up to ``num_tokens`` query
+    tokens in ``batch`` sequences (callers that capture graphs keep one)."""
+    nbytes = extend_workspace_bytes(num_tokens, num_q_heads, num_kv_heads, batch)
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
 
 
 def _i32(t: torch.Tensor) -> torch.Tensor:
@@ -329,19 +343,22 @@ def paged_forward(
         if hkv != int(num_kv_heads):
             raise ValueError(f"num_kv_heads {num_kv_heads} does not match the cache ({hkv})")
     B = seq_lens.shape[0]
-    if max_q_len_hint is None:
-        max_q_len_hint = int((query_start_loc[1:] - query_start_loc[:-1]).max().item()) if B else 0
-    if linear_verify and 0 < max_q_len_hint <= VERIFY_MAX_Q_PER_SEQ:
-        return paged_verify_forward(
-            q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
-            max_q_per_seq=max_q_len_hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
-            causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
-            page_size=block_size, max_seq_len_hint=max_seq_len_hint, workspace=workspace)
+    if linear_verify:
+        if max_q_len_hint is None:
+            # the verifier's grid needs the longest chain (the reference reads the same
+            # bound from the host, _paged_adapter.py:613-617)
+            max_q_len_hint = int((query_start_loc[1:] - query_start_loc[:-1]).max().item()) if B else 0
+        if 0 < max_q_len_hint <= VERIFY_MAX_Q_PER_SEQ:
+            return paged_verify_forward(
+                q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
+                max_q_per_seq=max_q_len_hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
+                causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
+                page_size=block_size, max_seq_len_hint=max_seq_len_hint, workspace=workspace)
     return paged_extend_forward(
         q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
-        max_q_len=max_q_len_hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
+        softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
         causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
-        page_size=block_size)
+        page_size=block_size, workspace=workspace)
 
 
 def paged_extend_forward(
@@ -353,7 +370,6 @@ def paged_extend_forward(
     query_start_loc: torch.Tensor,
     prefix_kv_lens: Optional[torch.Tensor],
     *,
-    max_q_len: int,
     softmax_scale: float,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
@@ -362,8 +378,13 @@ def paged_extend_forward(
     out: Optional[torch.Tensor] = None,
     row_index: Optional[torch.Tensor] = None,
     page_size: Optional[int] = None,
+    workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Prefix-aware extend on MFMA tiles: ``q`` [num_tokens, Hq, D] -> ``out`` (q's dtype)."""
+    """Prefix-aware extend on MFMA tiles: ``q`` [num_tokens, Hq, D] -> ``out`` (q's dtype).
+
+    The row tiles are listed on the device, so no host value of the query lengths is
+    read. ``workspace`` (uint8, ``extend_workspace``) defaults to the shared buffer of
+    the current stream; a split-KV workspace of enough bytes serves as well."""
     if q.dim() != 3:
         raise ValueError(f"q must be [tokens, heads, head_dim], got {tuple(q.shape)}")
     if v_cache.dtype != k_cache.dtype:
@@ -387,13 +408,21 @@ def paged_extend_forward(
     qsl = _i32(query_start_loc)
     pre = None if prefix_kv_lens is None else _i32(prefix_kv_lens)
     ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
-    status = _lib.load().ma_paged_extend(
+    lib = _lib.load()
+    nbytes = lib.ma_extend_workspace_bytes(T, Hq, Hkv, B)
+    if workspace is None:
+        ws = workspace_buffer(dev, nbytes)
+    else:
+        if workspace.dtype != torch.uint8 or workspace.device != dev or workspace.numel() < nbytes:
+            raise ValueError(f"workspace must be a uint8 tensor of at least {nbytes} bytes on {dev}")
+        ws = workspace
+    status = lib.ma_paged_extend(
         q.data_ptr(), q.stride(0), q.stride(1), q_dtype_code(q.dtype), T,
         k_cache.data_ptr(), v_cache.data_ptr(), row, head, kv_dtype_code(k_cache.dtype),
         table.data_ptr(), table.stride(0), _ptr(ridx), ps,
         seq.data_ptr(), qsl.data_ptr(), _ptr(pre),
-        B, int(max_q_len), Hq, Hkv, D, 1 if causal else 0, int(sliding_window_size),
-        float(softmax_scale), float(k_scale), float(v_scale),
+        B, Hq, Hkv, D, 1 if causal else 0, int(sliding_window_size),
+        float(softmax_scale), float(k_scale), float(v_scale), _ptr(ws), nbytes,
         out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
     )
     _lib.check(status, "ma_paged_extend")

@@ -8,8 +8,14 @@
 // Decomposition: one workgroup = 8 waves = 256 query rows of ONE kv head, where row r of
 // a sequence is (query token r / G, GQA head r % G); each wave owns 32 rows (two 16-row
 // blocks), two waves per SIMD so that one's softmax overlaps the other's MFMAs. All G
-// heads that share a kv head are served from one copy of each K/V tile in LDS. Row tiles
-// are launched heaviest-first (the last tokens of a causal sequence see the most keys).
+// heads that share a kv head are served from one copy of each K/V tile in LDS.
+//
+// Work list: a one-workgroup plan kernel lists the row tiles (sequence, tile) of the
+// batch from query_start_loc on the device, ordered by their key-tile count, heaviest
+// first (a longest-processing-time order over the CUs), so no host-side maximum of the
+// query lengths is needed. The extend grid is 1-D, (list entry) x (kv head) with the kv
+// head fastest: workgroup i runs on XCD i % 8, so with 8 kv heads each XCD streams one
+// head's K/V through its own L2.
 //
 // Per 64-key tile, per wave (scores of all 64 keys, then one online-softmax update, then
 // PV), MFMA 16x16x32 with fp32 accumulate:
@@ -46,6 +52,12 @@ constexpr int kXBM = kXWaves * kXRB * 16;      // query rows per workgroup
 constexpr int kXBN = 64;                       // keys per tile
 constexpr int kXD = 128;                       // head dim
 
+// One entry of the work list: sequence in the low 32 bits, row tile in the high 32;
+// -1 (sequence -1) past the last tile.
+__host__ __device__ constexpr int64_t row_tile_item(int seq, int tile) {
+  return (int64_t)(((uint64_t)(uint32_t)tile << 32) | (uint32_t)seq);
+}
+
 struct ExtendArgs {
   const void* q;
   int64_t q_stride_tok, q_stride_head;
@@ -58,13 +70,156 @@ struct ExtendArgs {
   const int32_t* qsl;
   const int32_t* prefix;
   int batch, hq, hkv, group;
-  int row_tiles;      // row tiles per (sequence, kv head) in the grid
+  const int64_t* items;  // work list (row_tile_item)
   int causal, window;
   float scale_log2;
   float v_scale;
   void* out;
   int64_t out_stride_tok, out_stride_head;
 };
+
+// Keys [lo, hi) that some row of the row tile starting at row r0 of a sequence may see.
+struct KeyRange {
+  int lo, hi;
+};
+__device__ __forceinline__ KeyRange row_tile_keys(int r0, int ntok, int group, int prefix, int seq, int causal,
+                                                  int window) {
+  const int t_first = r0 / group;
+  const int t_last = min(ntok - 1, (r0 + kXBM - 1) / group);
+  KeyRange k;
+  k.lo = window >= 0 ? max(0, prefix + t_first - window) : 0;
+  k.hi = causal ? min(seq, prefix + t_last + 1) : seq;
+  return k;
+}
+
+// ---- work list ----
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanBuckets = 1024;      // cost classes of the counting sort
+constexpr int kPlanMaxBatch = 16384;    // per-sequence tile offsets kept in LDS
+constexpr int kPlanFixedCost = 2;       // a row tile's set-up, in key tiles
+
+struct ExtendPlanArgs {
+  const int32_t* qsl;
+  const int32_t* seq_lens;
+  const int32_t* prefix;
+  int batch, group, causal, window;
+  int capacity;  // entries of items
+  int64_t* items;
+};
+
+// Row tiles of a sequence with ntok query tokens.
+__device__ __forceinline__ int seq_row_tiles(int ntok, int group) {
+  return ntok > 0 ? (int)(((int64_t)ntok * group + kXBM - 1) / kXBM) : 0;
+}
+
+// Block-wide exclusive prefix sum of one value per thread (kPlanThreads threads);
+// returns this thread's offset and sets *total. Uses sums[kPlanThreads / 64].
+__device__ __forceinline__ int block_exclusive_scan(int x, int* sums, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int incl = x;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  if (lane == 63) sums[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanThreads / 64; ++w) {
+    const int s = sums[w];
+    before += (w < wave) ? s : 0;
+    all += s;
+  }
+  __syncthreads();  // sums is free again
+  *total = all;
+  return before + incl - x;
+}
+
+// One workgroup: list every row tile of the batch as {sequence, tile}, the ones with the
+// most key tiles first (a counting sort over kPlanBuckets cost classes), and fill the
+// rest of items with {-1, -1}. The order within a class is arbitrary; each row tile's
+// result does not depend on it.
+__global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const ExtendPlanArgs a) {
+  __shared__ int start[kPlanMaxBatch + 1];
+  __shared__ int hist[kPlanBuckets];
+  __shared__ int sums[kPlanThreads / 64];
+  static_assert(kPlanBuckets == kPlanThreads, "one cost class per thread in the scan");
+  const int tid = threadIdx.x;
+  const int32_t MA_GLOBAL* qsl = gptr(a.qsl);
+  const int32_t MA_GLOBAL* seq_lens = gptr(a.seq_lens);
+
+  // 1. first list index of each sequence's row tiles
+  int carry = 0;
+  for (int base = 0; base < a.batch; base += kPlanThreads) {
+    const int b = base + tid;
+    const int n = b < a.batch ? seq_row_tiles(qsl[b + 1] - qsl[b], a.group) : 0;
+    int total;
+    const int off = block_exclusive_scan(n, sums, &total);
+    if (b < a.batch) start[b] = carry + off;
+    carry += total;
+  }
+  const int m = carry;  // the same in every thread
+  if (tid == 0) start[a.batch] = m;
+  hist[tid] = 0;
+  __syncthreads();
+
+  // list index t -> (sequence, row tile) and its cost in key tiles
+  auto decode = [&](int t, int* b_out, int* rt_out) -> int {
+    int lo = 0, hi = a.batch;  // the last b with start[b] <= t (start[batch] = m > t)
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (start[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int b = lo;
+    const int rt = t - start[b];
+    const int ntok = qsl[b + 1] - qsl[b];
+    const int seq = seq_lens[b];
+    const int prefix = a.prefix ? gptr(a.prefix)[b] : seq - ntok;
+    const KeyRange k = row_tile_keys(rt * kXBM, ntok, a.group, prefix, seq, a.causal, a.window);
+    *b_out = b;
+    *rt_out = rt;
+    return (k.hi > k.lo ? (k.hi - k.lo + kXBN - 1) / kXBN : 0) + kPlanFixedCost;
+  };
+
+  // 2. the largest cost, which scales the classes
+  int cmax = 0;
+  for (int t = tid; t < m; t += kPlanThreads) {
+    int b, rt;
+    cmax = max(cmax, decode(t, &b, &rt));
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) cmax = max(cmax, __shfl_xor(cmax, d, 64));
+  if ((tid & 63) == 0) sums[tid >> 6] = cmax;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kPlanThreads / 64; ++w) cmax = max(cmax, sums[w]);
+  __syncthreads();
+
+  // 3. class sizes (class 0 holds the heaviest tiles), 4. their first list index
+  auto cls = [&](int cost) -> int {
+    return kPlanBuckets - 1 - (int)(((int64_t)cost * kPlanBuckets) / ((int64_t)cmax + 1));
+  };
+  for (int t = tid; t < m; t += kPlanThreads) {
+    int b, rt;
+    atomicAdd(&hist[cls(decode(t, &b, &rt))], 1);
+  }
+  __syncthreads();
+  int unused;
+  const int first = block_exclusive_scan(hist[tid], sums, &unused);
+  hist[tid] = first;
+  __syncthreads();
+
+  // 5. scatter, 6. pad
+  int64_t MA_GLOBAL* items = gptr_mut(a.items);
+  for (int t = tid; t < m; t += kPlanThreads) {
+    int b, rt;
+    const int pos = atomicAdd(&hist[cls(decode(t, &b, &rt))], 1);
+    if (pos < a.capacity) items[pos] = row_tile_item(b, rt);
+  }
+  for (int i = m + tid; i < a.capacity; i += kPlanThreads) items[i] = row_tile_item(-1, -1);
+}
 
 template <bool QBF16, int KV>
 __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArgs args) {
@@ -96,9 +251,12 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   const int c = lane & 15;
   const int j = lane >> 4;
 
-  const int rt = a.row_tiles - 1 - (int)blockIdx.x;  // heaviest row tiles first
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  const int item = (int)blockIdx.x / a.hkv;
+  const int h = (int)blockIdx.x - item * a.hkv;
+  const int64_t work = cptr(a.items)[item];
+  const int b = (int)(uint32_t)work;
+  if (b < 0) return;
+  const int rt = (int)(work >> 32);
   const int tok0 = cptr(a.qsl)[b];
   const int ntok = cptr(a.qsl)[b + 1] - tok0;
   const int r0 = rt * kXBM;
@@ -130,8 +288,9 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   // keys any row of the workgroup may see, and the window in which no row needs masking
   const int t_first = r0 / a.group;
   const int t_last = min(ntok - 1, (r0 + kXBM - 1) / a.group);
-  const int key_lo = a.window >= 0 ? max(0, prefix + t_first - a.window) : 0;
-  const int key_hi = a.causal ? min(seq, prefix + t_last + 1) : seq;
+  const KeyRange keys = row_tile_keys(r0, ntok, a.group, prefix, seq, a.causal, a.window);
+  const int key_lo = keys.lo;
+  const int key_hi = keys.hi;
   const int full_lo = a.window >= 0 ? max(0, prefix + t_last - a.window) : 0;
   const int full_hi = a.causal ? min(seq, prefix + t_first + 1) : seq;
   const int ntiles = key_hi > key_lo ? (key_hi - key_lo + kXBN - 1) / kXBN : 0;
@@ -424,14 +583,26 @@ static hipError_t launch_extend_q(int kv, dim3 grid, hipStream_t st, const Exten
 
 using namespace ma;
 
+static int64_t extend_items(int64_t num_tokens, int group, int batch) {
+  // sum over sequences of ceil(ntok * G / kXBM) <= num_tokens * G / kXBM + batch
+  return (num_tokens * group + kXBM - 1) / kXBM + batch;
+}
+
+extern "C" size_t ma_extend_workspace_bytes(int64_t num_tokens, int num_q_heads, int num_kv_heads, int batch) {
+  if (num_tokens < 0 || batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return 0;
+  const int64_t n = extend_items(num_tokens, num_q_heads / num_kv_heads, batch);
+  return ((size_t)n * sizeof(int64_t) + 255) & ~(size_t)255;
+}
+
 extern "C" int ma_paged_extend(
     const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype, int64_t num_tokens,
     const void* k_cache, const void* v_cache, int64_t kv_stride_row, int64_t kv_stride_head, int kv_dtype,
     const int32_t* table, int64_t table_stride, const int64_t* row_index, int page_size,
     const int32_t* seq_lens, const int32_t* query_start_loc, const int32_t* prefix_lens,
-    int batch, int max_q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
+    int batch, int num_q_heads, int num_kv_heads, int head_dim,
     int causal, int sliding_window, float softmax_scale, float k_scale, float v_scale,
-    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+    void* workspace, size_t workspace_bytes, void* out, int64_t out_stride_tok, int64_t out_stride_head,
+    void* stream) {
   if (head_dim != kXD) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (128)", head_dim);
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
   if (kv_dtype < 0 || kv_dtype > DT_E5M2) return set_error(MA_EINVAL, "kv dtype %d unknown", kv_dtype);
@@ -441,8 +612,9 @@ extern "C" int ma_paged_extend(
     return set_error(MA_EINVAL, "bad head counts hq=%d hkv=%d", num_q_heads, num_kv_heads);
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
   if (!(softmax_scale * k_scale > 0.f)) return set_error(MA_EINVAL, "softmax scale must be positive");
-  if (max_q_per_seq < 0) return set_error(MA_EINVAL, "max query rows per sequence must be >= 0");
-  if (batch == 0 || max_q_per_seq == 0 || num_tokens == 0) return MA_OK;
+  if (num_tokens < 0) return set_error(MA_EINVAL, "num_tokens must be >= 0");
+  if (batch > kPlanMaxBatch) return set_error(MA_EUNSUPPORTED, "batch %d exceeds %d sequences", batch, kPlanMaxBatch);
+  if (batch == 0 || num_tokens == 0) return MA_OK;
   if (!q || !k_cache || !v_cache || !table || !seq_lens || !query_start_loc || !out)
     return set_error(MA_EINVAL, "null pointer argument");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache) |
@@ -452,20 +624,33 @@ extern "C" int ma_paged_extend(
   if (((kv_stride_row * elt) & 15) || ((kv_stride_head * elt) & 15) || ((q_stride_tok * 2) & 15) ||
       ((q_stride_head * 2) & 15) || ((out_stride_tok * 2) & 7) || ((out_stride_head * 2) & 7))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
+  const int group = num_q_heads / num_kv_heads;
+  const int64_t items = extend_items(num_tokens, group, batch);
+  if (items * num_kv_heads > 0x7fffffff / (kXWaves * 64)) return set_error(MA_EINVAL, "grid too large");
+  const size_t need = ma_extend_workspace_bytes(num_tokens, num_q_heads, num_kv_heads, batch);
+  if (!workspace || workspace_bytes < need)
+    return set_error(MA_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255) return set_error(MA_EINVAL, "workspace must be 256-byte aligned");
+  ExtendPlanArgs p{};
+  p.qsl = query_start_loc; p.seq_lens = seq_lens; p.prefix = prefix_lens;
+  p.batch = batch; p.group = group; p.causal = causal ? 1 : 0; p.window = sliding_window < 0 ? -1 : sliding_window;
+  p.capacity = (int)items; p.items = reinterpret_cast<int64_t*>(workspace);
+  hipLaunchKernelGGL(extend_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(MA_ELAUNCH, "extend plan launch failed: %s", hipGetErrorString(e));
   ExtendArgs a{};
   a.q = q; a.q_stride_tok = q_stride_tok; a.q_stride_head = q_stride_head;
   a.k = k_cache; a.v = v_cache; a.kv_stride_row = kv_stride_row; a.kv_stride_head = kv_stride_head;
   a.tt.table = table; a.tt.stride = table_stride; a.tt.page_shift = __builtin_ctz(page_size);
   a.row_index = row_index; a.seq_lens = seq_lens; a.qsl = query_start_loc; a.prefix = prefix_lens;
-  a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = num_q_heads / num_kv_heads;
-  a.row_tiles = (int)(((int64_t)max_q_per_seq * a.group + kXBM - 1) / kXBM);
-  a.causal = causal ? 1 : 0; a.window = sliding_window < 0 ? -1 : sliding_window;
+  a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group;
+  a.items = p.items;
+  a.causal = p.causal; a.window = p.window;
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
-  if (batch > 65535 || num_kv_heads > 65535) return set_error(MA_EINVAL, "grid too large");
-  dim3 grid(a.row_tiles, num_kv_heads, batch);
-  hipError_t e = (q_dtype == DT_BF16) ? launch_extend_q<true>(kv_dtype, grid, (hipStream_t)stream, a)
-                                      : launch_extend_q<false>(kv_dtype, grid, (hipStream_t)stream, a);
+  const dim3 grid((unsigned)(items * num_kv_heads));
+  e = (q_dtype == DT_BF16) ? launch_extend_q<true>(kv_dtype, grid, (hipStream_t)stream, a)
+                           : launch_extend_q<false>(kv_dtype, grid, (hipStream_t)stream, a);
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "extend launch failed: %s", hipGetErrorString(e));
   return MA_OK;
 }

@@ -113,3 +113,43 @@ def test_kv_write_rejects_bad_arguments(lib, over, msg):
 
 def test_kv_write_of_nothing_is_a_no_op(lib):
     assert lib.ma_set_kv_buffer(*_kvw_args(T=0)) == 0
+
+
+def _extend_args(**over):
+    args = dict(q=1 << 20, qs0=1024, qs1=128, qdt=1, T=64, k=1 << 21, v=1 << 22, rs=1024, hs=128, kvdt=1,
+                table=1 << 23, tstride=64, rowidx=None, ps=1, seq=1 << 24, qsl=1 << 25, pre=None,
+                batch=2, hq=16, hkv=2, dim=128, causal=1, win=-1, sm=0.1, ks=1.0, vs=1.0,
+                ws=1 << 26, wsb=1 << 12, out=1 << 27, os0=1024, os1=128, stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("over,msg", [
+    ({"dim": 64}, "head_dim"),
+    ({"qdt": 3}, "q dtype"),
+    ({"kvdt": 0}, "16-bit KV dtype must equal"),
+    ({"hq": 12, "hkv": 8}, "head counts"),
+    ({"ps": 6}, "power of two"),
+    ({"sm": -1.0}, "scale"),
+    ({"T": -1}, "num_tokens"),
+    ({"batch": 16385}, "exceeds"),
+    ({"out": (1 << 27) + 8}, "aligned"),
+    ({"ws": None}, "workspace too small"),
+    ({"wsb": 8}, "workspace too small"),
+    ({"ws": (1 << 26) + 64}, "256-byte aligned"),
+])
+def test_extend_rejects_bad_arguments(lib, over, msg):
+    assert lib.ma_paged_extend(*_extend_args(**over)) != 0
+    assert msg in lib.ma_last_error().decode()
+
+
+def test_extend_of_nothing_is_a_no_op(lib):
+    assert lib.ma_paged_extend(*_extend_args(T=0)) == 0
+    assert lib.ma_paged_extend(*_extend_args(batch=0)) == 0
+
+
+def test_extend_workspace_covers_every_row_tile(lib):
+    # 256-row tiles: sum over sequences of ceil(E_b * G / 256) <= ceil(T * G / 256) + B
+    assert lib.ma_extend_workspace_bytes(1000, 40, 8, 3) == 256
+    assert lib.ma_extend_workspace_bytes(100000, 64, 8, 300) == ((3125 + 300) * 8 + 255) // 256 * 256
+    assert lib.ma_extend_workspace_bytes(10, 12, 8, 1) == 0

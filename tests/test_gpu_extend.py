@@ -32,6 +32,8 @@ def _check_rows(q, k_pool, v_pool, slots_of, prefix, qsl, out, rows_of, scale, k
     """Check the listed query rows of each sequence; rows become one-row problems for the oracle."""
     qf = to_f64(q)
     for b, rows in rows_of.items():
+        if not rows:
+            continue
         n_total = int(prefix[b]) + (int(qsl[b + 1]) - int(qsl[b]))
         slots = torch.as_tensor(slots_of(b, n_total), dtype=torch.int64, device=k_pool.device)
         kb, vb = _gather_f64(k_pool, slots), _gather_f64(v_pool, slots)
@@ -155,3 +157,44 @@ def test_extend_fp16(gpu):
 def test_extend_page_size_16_table(gpu):
     """Reference layout [pages, 16, Hkv, D] with scattered pages (tests/test_attention_v100_gpu.py shapes)."""
     _run_synthetic(gpu, [64, 0], [32, 48], 8, 2, dtype=torch.float16, page_size=16)
+
+
+def test_extend_ragged_batch_with_empty_sequences(gpu):
+    # sequences without new tokens list no row tile; the others must still be served
+    _run_synthetic(gpu, [30, 0, 400, 9, 0], [0, 70, 0, 300, 1], 40, 8)
+
+
+def test_extend_more_sequences_than_one_scan_pass(gpu):
+    """1,100 sequences: the work list's prefix sum over sequences runs in two passes."""
+    g = torch.Generator().manual_seed(5)
+    B = 1100
+    extend = torch.randint(0, 4, (B,), generator=g).tolist()
+    prefix = torch.randint(0, 90, (B,), generator=g).tolist()
+    _run_synthetic(gpu, prefix, extend, 16, 8)
+
+
+def test_extend_work_list_lists_every_row_tile_heaviest_first(gpu):
+    prefix, extend, heads, heads_kv = [0, 3000, 17, 800, 0], [700, 40, 0, 1500, 5], 40, 8
+    q, k, v, table, seq, qsl = _synthetic(gpu, prefix, extend, heads, heads_kv)
+    ops = _ops()
+    B, T, G = len(prefix), q.shape[0], heads // heads_kv
+    ws = ops.extend_workspace(q.device, T, heads, heads_kv, B)
+    ws.fill_(0x5A)
+    ops.paged_extend_forward(
+        q, k, v, table.to(gpu), torch.tensor(seq, dtype=torch.int32, device=gpu),
+        torch.tensor(qsl, dtype=torch.int32, device=gpu), torch.tensor(prefix, dtype=torch.int32, device=gpu),
+        softmax_scale=128 ** -0.5, workspace=ws)
+    torch.cuda.synchronize()
+    cap = (T * G + 255) // 256 + B
+    items = ws[: cap * 8].view(torch.int64).cpu().tolist()
+    listed = [(it & 0xFFFFFFFF, it >> 32) for it in items if it != -1]
+    assert all(it == -1 for it in items[len(listed):]), "padding must follow the listed tiles"
+    want = sorted((b, rt) for b in range(B) for rt in range((extend[b] * G + 255) // 256))
+    assert sorted(listed) == want
+
+    def key_tiles(b, rt):  # keys of the tile's last row: causal, no window
+        t_last = min(extend[b] - 1, (rt * 256 + 255) // G)
+        return (min(seq[b], prefix[b] + t_last + 1) + 63) // 64
+
+    costs = [key_tiles(b, rt) for b, rt in listed]
+    assert costs == sorted(costs, reverse=True)

@@ -56,7 +56,7 @@ def test_extend_and_verify_match_fixture(name, kernel):
     ops = _ops()
     if kernel == "extend":
         out = ops.paged_extend_forward(d["q"], d["k"], d["v"], d["r2t"], d["seq"], d["qsl"], d["pre"],
-                                       max_q_len=max(qlens), **common)
+                                       **common)
     else:
         out = ops.paged_verify_forward(d["q"], d["k"], d["v"], d["r2t"], d["seq"], d["qsl"], d["pre"],
                                        max_q_per_seq=max(qlens), **common)
