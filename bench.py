@@ -14,7 +14,9 @@ resident in HBM:
   of the same JSON line.
 
 ``value`` is whole-job throughput: algorithmic bytes of the K timed steps over
-the wall time between the two synchronisations. ``roofline`` compares the
+the wall time between the two synchronisations. Warm-up is W untimed steps and
+then more untimed steps until half a second has passed, so that the timed steps
+run at settled clocks. ``roofline`` compares the
 algorithmic bytes of one call with its HIP-event duration on the launch stream
 against the 8 TB/s HBM peak; ``roofline.traffic`` is the measured HBM bytes per
 launch of the dominant kernel, read from the committed counter summary
@@ -111,12 +113,23 @@ def _runner(w):
         max_seq_len_hint=hint, max_q_len_hint=T)
 
 
+WARMUP_MIN_S = 0.5
+
+
 def _time_gpu(fn, steps, warmup):
+    """Run ``warmup`` untimed steps, and more until WARMUP_MIN_S of wall time has passed
+    (the GPU's clocks settle under sustained load; a few sub-millisecond calls do not get
+    there), then time ``steps`` steps."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t_end = time.perf_counter() + WARMUP_MIN_S
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
@@ -283,6 +296,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_s": WARMUP_MIN_S,
         "ms_per_step": round(head["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
