@@ -76,6 +76,50 @@ def _calibrate_copy(mib):
                       "GBps_read_plus_write": 2 * n / dt / 1e9}))
 
 
+GATHER_ORDERS = {0: "random slots, head-major", 1: "random slots, head-minor", 2: "in order"}
+
+
+def _gather_ceiling(num_tokens, heads, row_bytes, order, steps=20):
+    """Read bandwidth of a plain gather of ``num_tokens * heads`` rows of ``row_bytes``
+    (libma_calibrate.so, csrc/calibrate/gather_ceiling.hip): the attainable rate of the
+    KV access pattern without any attention arithmetic. Returns GB/s."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "sglang_restomod_amd", "libma_calibrate.so")
+    lib = ctypes.CDLL(path)
+    lib.ma_gather_ceiling_blocks.restype = ctypes.c_int64
+    lib.ma_gather_ceiling_blocks.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.ma_gather_ceiling.restype = ctypes.c_int
+    lib.ma_gather_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    pool = torch.randint(0, 256, (num_tokens * heads * row_bytes,), dtype=torch.uint8, device=dev, generator=g)
+    perm = torch.randperm(num_tokens, device=dev, generator=g).to(torch.int32)
+    rows_per_wave = 64
+    blocks = lib.ma_gather_ceiling_blocks(num_tokens, heads, row_bytes, rows_per_wave)
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run():
+        rc = lib.ma_gather_ceiling(pool.data_ptr(), perm.data_ptr(), num_tokens, heads, row_bytes, order,
+                                   rows_per_wave, sink.data_ptr(), sink.numel(), stream)
+        if rc != 0:
+            raise RuntimeError(f"ma_gather_ceiling failed ({rc})")
+
+    _, per = _time_gpu(run, steps, 5)
+    ms = statistics.median(per)
+    del pool, perm, sink
+    torch.cuda.empty_cache()
+    return pool_bytes(num_tokens, heads, row_bytes) / (ms * 1e-3) / 1e9
+
+
+def pool_bytes(num_tokens, heads, row_bytes):
+    return num_tokens * heads * row_bytes
+
+
 def _traffic(kernel, workload):
     """HBM bytes per launch of `kernel` on `workload` from its committed counter summary."""
     import re
@@ -258,6 +302,12 @@ def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
     }
     res["hbm_frac"] = res["GBps"] / HBM_PEAK_GBS
     res["mfma_frac"] = res["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
+    if w.mode != "extend":
+        # the same number of K and V rows, gathered from random slots with no arithmetic
+        row_bytes = w.dim * w.k_pool.element_size()
+        tokens = 2 * int(sum(w.seq_lens_cpu))
+        res["gather_ceiling_GBps"] = _gather_ceiling(tokens, w.heads_kv, row_bytes, 0)
+        res["gather_row_bytes"] = row_bytes
     if cpu_baseline:
         med, frac, cores, rows = _cpu_baseline(w, cpu_seconds)
         sub_bytes = nbytes * frac if w.mode == "decode" else None
@@ -317,6 +367,14 @@ def main():
                        if bound_hbm else "HIP events on the launch stream around each call"),
         },
     }
+    if bound_hbm:
+        ceil = head["gather_ceiling_GBps"]
+        line["roofline"]["gather_ceiling"] = {
+            "GBps": round(ceil, 1),
+            "frac": round(head["GBps"] / ceil, 4),
+            "pattern": f"the same K and V rows ({head['gather_row_bytes']} B per token and kv head) gathered from "
+                       f"random pool slots by a plain load kernel, measured in this run",
+        }
     if "cpu" in head:
         c = head["cpu"]
         line["cpu_baseline"] = {

@@ -3,7 +3,8 @@
     python -m sglang_restomod_amd.build        (or __graft_entry__.build())
 
 Each source compiles to an object under csrc/_build/ in parallel, then one
-hipcc link produces sglang_restomod_amd/libmi355x_attn.so. Packed fp32 VALU
+hipcc link produces sglang_restomod_amd/libmi355x_attn.so. The measurement
+kernels of csrc/calibrate/ link into libma_calibrate.so (used by bench.py only). Packed fp32 VALU
 instructions are disabled for device code (-packed-fp32-ops).
 """
 
@@ -19,6 +20,9 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libmi355x_attn.so"
+# measurement kernels for bench.py, linked apart from the attention library
+CALIB_SRC = CSRC / "calibrate"
+CALIB_OUT = PKG / "libma_calibrate.so"
 ARCH = os.environ.get("MI355X_ATTN_ARCH", "gfx950")
 
 
@@ -98,13 +102,24 @@ def build(verbose: bool = False, extra: list[str] | None = None, jobs: int | Non
                 print(err, file=sys.stderr)
         for src, f in zip(srcs, asms):
             verify_assembly(src, f.result())
-    tmp = OUT.with_suffix(".so.tmp")
+    _link(objs, OUT)
+    calib = sorted(CALIB_SRC.glob("*.hip"))
+    if calib:
+        cobjs = []
+        for src in calib:
+            cobjs.append(_compile(src, bdir / ("calibrate_" + src.stem + ".o"), extra)[0])
+            verify_assembly(src, _assembly(src, extra))
+        _link(cobjs, CALIB_OUT)
+    return OUT
+
+
+def _link(objs: list[Path], out: Path) -> None:
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
 
 
 if __name__ == "__main__":
