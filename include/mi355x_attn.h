@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 5
+#define MA_ABI_VERSION 6
 
 /* dtype codes */
 #define MA_DT_F16 0
@@ -177,6 +177,39 @@ int ma_set_kv_buffer(const void* k, const void* v, int64_t src_stride_tok, int64
                      int head_dim, void* k_cache, void* v_cache, int64_t cache_stride_row,
                      int64_t cache_stride_head, int cache_dtype, int64_t num_slots, float k_scale,
                      float v_scale, int apply_scale, void* stream);
+
+/*
+ * Token-table rows translated through a slot mapping, on the device.
+ * Replaces the sliding-window page-table build (flash_attn_v100_backend.py:460-503:
+ * req_to_token rows up to the longest sequence, read with seq_lens.max().item(), then
+ * the pool's translate_loc_from_full_to_swa):
+ *   out[b * out_stride + j] = mapping[table[r * table_stride + j]] for
+ *   j < min(seq_lens[b], width), r = row_index ? row_index[b] : b.
+ * mapping is int64 [mapping_len] (the SWA pool's full_to_swa_index_mapping); a slot
+ * outside [0, mapping_len) gives 0. Positions from seq_lens[b] on are not written.
+ * batch <= 65535; out_stride >= width.
+ */
+int ma_translate_slots(const int32_t* table, int64_t table_stride, const int64_t* row_index,
+                       const int32_t* seq_lens, int batch, const int64_t* mapping, int64_t mapping_len,
+                       int32_t* out, int64_t out_stride, int width, void* stream);
+
+/*
+ * fp8 paged KV decoded into fp16 logical pages.
+ * Replaces gather_fp8_paged_kv (_paged_adapter.py:527-564, _kernels_fp8_bridge.py:20-70):
+ * for logical page p < ceil(seq_lens[b] / page_size) of sequence b, physical page
+ * page_table[b * table_stride + p] of k_cache / v_cache (fp8 bytes, [num_pages,
+ * page_size, num_kv_heads, head_dim] with the given byte strides) is decoded into page
+ * b * max_blocks + p of k_out / v_out (fp16, contiguous [batch * max_blocks, page_size,
+ * num_kv_heads, head_dim]). kv_dtype MA_DT_E4M3 or MA_DT_E5M2; decoding is exact (e5m2:
+ * the byte shifted into the high half, NaN payloads included). Other output pages and
+ * physical pages outside [0, num_pages) are left untouched. head_dim a multiple of 16;
+ * caches, outputs and strides 16-byte aligned.
+ */
+int ma_gather_fp8_paged_kv(const void* k_cache, const void* v_cache, int64_t stride_page, int64_t stride_tok,
+                           int64_t stride_head, int kv_dtype, int64_t num_pages, const int32_t* page_table,
+                           int64_t table_stride, const int32_t* seq_lens, int batch, int max_blocks,
+                           int page_size, int num_kv_heads, int head_dim, void* k_out, void* v_out,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -56,6 +56,17 @@ SIGNATURES = {
         c_void_p, c_void_p, c_int64, c_int64, c_int,  # caches, strides, cache dtype
         c_int64, c_float, c_float, c_int, c_void_p,   # num_slots, scales, apply, stream
     ]),
+    "ma_translate_slots": (c_int, [
+        c_void_p, c_int64, c_void_p, c_void_p, c_int,  # table, stride, row_index, seq_lens, batch
+        c_void_p, c_int64,                            # mapping, mapping_len
+        c_void_p, c_int64, c_int, c_void_p,           # out, stride, width, stream
+    ]),
+    "ma_gather_fp8_paged_kv": (c_int, [
+        c_void_p, c_void_p, c_int64, c_int64, c_int64,  # caches, page/token/head strides (bytes)
+        c_int, c_int64, c_void_p, c_int64, c_void_p,  # dtype, num_pages, page_table, stride, seq_lens
+        c_int, c_int, c_int, c_int, c_int,            # batch, max_blocks, page_size, hkv, dim
+        c_void_p, c_void_p, c_void_p,                 # k_out, v_out, stream
+    ]),
     "ma_extend_workspace_bytes": (c_size_t, [c_int64, c_int, c_int, c_int]),
     "ma_paged_extend": (c_int, [
         c_void_p, c_int64, c_int64, c_int, c_int64,   # q, strides, dtype, num_tokens

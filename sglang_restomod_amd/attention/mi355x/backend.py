@@ -17,9 +17,11 @@ What differs by design:
 * The kernels address SGLang's ``req_to_token`` directly (page size 1,
   ``req_pool_indices`` as the row index), so the metadata is the engine's own
   tensors plus ``query_start_loc`` and the prefix lengths: no page table is built
-  and nothing synchronises with the host when the engine supplies
-  ``extend_seq_lens_cpu`` (the reference reads ``seq_lens.max().item()`` here,
-  :457).
+  and nothing synchronises with the host (the reference reads
+  ``seq_lens.max().item()`` here, :457). The extend kernel lists its row tiles on
+  the device, and the sliding-window table of an SWA pool is translated on the
+  device row by row (``ops.translate_slots``). Only a draft extend without
+  ``extend_seq_lens_cpu`` reads its longest chain from the device, to route it.
 * fp8 KV (e4m3fn / e5m2, per-tensor scale) is read directly by every kernel; the
   reference's fp16 prefill scratch (:277-330, gather at :1226-1253) is not needed.
 """
@@ -152,21 +154,15 @@ class MI355XAttnBackend(_EngineBase):
     # ------------------------------------------------------------------
     # Metadata (reference: _build_extend_metadata :432-565, init_forward_metadata :567-621)
     # ------------------------------------------------------------------
-    def _swa_rows(self, row_index: torch.Tensor, width: int,
+    def _swa_rows(self, row_index: torch.Tensor, seq_lens: torch.Tensor,
                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """req_to_token rows translated to SWA-pool slots, [B, width] int32."""
-        pos = torch.arange(width, device=self.req_to_token.device)
-        slots = self.req_to_token[row_index[:, None], pos[None, :]]
-        swa = self.token_to_kv_pool.translate_loc_from_full_to_swa(slots).to(torch.int32)
-        if out is None:
-            return swa.contiguous()
-        out[: swa.shape[0], :width].copy_(swa)
-        return out[: swa.shape[0]]
-
-    def _max_len(self, seq_lens: torch.Tensor, seq_lens_cpu) -> int:
-        if seq_lens_cpu is not None and len(seq_lens_cpu):
-            return int(max(seq_lens_cpu))
-        return int(seq_lens.max().item()) if seq_lens.numel() else 0
+        """req_to_token rows translated to SWA-pool slots on the device, [B, width] int32,
+        each row up to its own length (reference :460-503 gathers up to the longest
+        sequence, read with .item())."""
+        width = int(self.req_to_token.shape[1]) if out is None else min(int(out.shape[1]),
+                                                                        int(self.req_to_token.shape[1]))
+        return ops.translate_slots(self.req_to_token, seq_lens, self.token_to_kv_pool.full_to_swa_index_mapping,
+                                   row_index=row_index, out=out, width=width)
 
     def build_metadata(
         self,
@@ -195,8 +191,7 @@ class MI355XAttnBackend(_EngineBase):
             # grid needs the longest chain, which callers pass (0: not known)
             md.max_q_per_seq = int(max_q_per_seq) if max_q_per_seq is not None else 0
         if self._has_swa_pool():
-            width = self._max_len(md.seq_lens, seq_lens_cpu if mode == MODE_DECODE else None)
-            md.swa_table = self._swa_rows(row_index, max(width, 1))
+            md.swa_table = self._swa_rows(row_index, md.seq_lens)
             md.swa_row_index = torch.arange(row_index.shape[0], dtype=torch.int64, device=row_index.device)
         return md
 
@@ -315,7 +310,7 @@ class MI355XAttnBackend(_EngineBase):
             prefix_kv_lens=self._cg_prefix_kv_lens[:bs], causal=True, max_q_per_seq=max_q,
             num_tokens=int(num_tokens))
         if self._cg_swa_table is not None:
-            md.swa_table = self._swa_rows(self._cg_row_index[:bs], self.max_context_len, out=self._cg_swa_table)
+            md.swa_table = self._swa_rows(self._cg_row_index[:bs], md.seq_lens, out=self._cg_swa_table)[:bs]
             md.swa_row_index = torch.arange(bs, dtype=torch.int64, device=self.device)
         self.forward_metadata = md
 

@@ -3,6 +3,8 @@
 * ``grouped_decode_forward`` - sglang_restomod/attention/v100/tilelang/_paged_adapter.py:402-486
 * ``paged_forward``          - _paged_adapter.py:567-759 (extend, and the linear-verify branch)
 * ``set_kv_buffer``          - the token pool's write called at flash_attn_v100_backend.py:1174-1182
+* ``gather_fp8_paged_kv``    - _paged_adapter.py:527-564
+* ``translate_slots``        - the SWA page-table build, flash_attn_v100_backend.py:460-503
 
 Shapes and dtypes are validated here and raise ``ValueError`` the way the
 reference's gates do (_paged_adapter.py:417-418, 538-541). Workspaces are
@@ -472,3 +474,68 @@ def set_kv_buffer(
         slots, ks, vs, 1 if apply else 0, _stream_ptr(dev),
     )
     _lib.check(status, "ma_set_kv_buffer")
+
+
+def translate_slots(
+    table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    mapping: torch.Tensor,
+    row_index: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    width: Optional[int] = None,
+) -> torch.Tensor:
+    """Rows of ``table`` (req_to_token, int32) translated through ``mapping`` (the SWA
+    pool's ``full_to_swa_index_mapping``), on the device: ``out[b, j] =
+    mapping[table[row_index[b], j]]`` for ``j < seq_lens[b]``; slots outside the mapping
+    give 0 and positions from ``seq_lens[b]`` on are left as they are. ``out`` defaults to
+    a new ``[B, width]`` int32 tensor, ``width`` to the table's width; no host value of
+    the lengths is read."""
+    if table.dtype != torch.int32 or table.dim() != 2 or table.stride(1) != 1:
+        raise ValueError("table must be a 2-D int32 tensor with contiguous rows")
+    dev = _check_device(table, seq_lens, mapping)
+    B = int(seq_lens.shape[0])
+    width = int(table.shape[1] if width is None else width)
+    if width > table.shape[1]:
+        raise ValueError(f"width {width} exceeds the table's {table.shape[1]} columns")
+    if out is None:
+        out = torch.empty(B, width, dtype=torch.int32, device=dev)
+    if out.dtype != torch.int32 or out.dim() != 2 or out.stride(1) != 1 or out.shape[0] < B or out.shape[1] < width:
+        raise ValueError(f"out must be an int32 [>= {B}, >= {width}] tensor with contiguous rows")
+    seq = _i32(seq_lens)
+    m64 = mapping if (mapping.dtype == torch.int64 and mapping.is_contiguous()) else mapping.to(torch.int64).contiguous()
+    ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
+    status = _lib.load().ma_translate_slots(
+        table.data_ptr(), table.stride(0), _ptr(ridx), seq.data_ptr(), B, m64.data_ptr(), m64.numel(),
+        out.data_ptr(), out.stride(0), width, _stream_ptr(dev))
+    _lib.check(status, "ma_translate_slots")
+    return out
+
+
+def gather_fp8_paged_kv(k_cache, v_cache, page_table, seq_lens, k_output, v_output) -> None:
+    """Resolve and decode the logical fp8 pages of each sequence into caller-owned fp16
+    buffers (reference: gather_fp8_paged_kv, same arguments and errors): caches
+    [num_pages, page_size, Hkv, D] in e4m3fn or e5m2, page_table [B, max_blocks],
+    outputs [B * max_blocks, page_size, Hkv, D] fp16; logical page p of sequence b
+    (p < ceil(seq_lens[b] / page_size)) goes to output page b * max_blocks + p."""
+    if k_cache.dtype not in FP8_DTYPES:
+        raise ValueError("gather_fp8_paged_kv expects E4M3 or E5M2 cache")
+    if v_cache.dtype != k_cache.dtype:
+        raise ValueError("K and V cache dtypes must match")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("caches must be [pages, page_size, heads, head_dim] of one layout")
+    if k_cache.stride(3) != 1:
+        raise ValueError("head_dim must be contiguous in the caches")
+    dev = _check_device(k_cache, v_cache, page_table, seq_lens, k_output, v_output)
+    num_pages, ps, hkv, d = k_cache.shape
+    B, max_blocks = page_table.shape
+    want = (B * max_blocks, ps, hkv, d)
+    for o in (k_output, v_output):
+        if tuple(o.shape) != want or o.dtype != torch.float16 or not o.is_contiguous():
+            raise ValueError(f"outputs must be contiguous float16 {want}")
+    table = _i32(page_table)
+    seq = _i32(seq_lens)
+    status = _lib.load().ma_gather_fp8_paged_kv(
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        kv_dtype_code(k_cache.dtype), num_pages, table.data_ptr(), table.stride(0), seq.data_ptr(),
+        B, max_blocks, ps, hkv, d, k_output.data_ptr(), v_output.data_ptr(), _stream_ptr(dev))
+    _lib.check(status, "ma_gather_fp8_paged_kv")

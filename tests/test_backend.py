@@ -154,16 +154,13 @@ def test_graph_batch_over_capacity_is_refused():
             3, 3, torch.zeros(3, dtype=torch.int64), torch.ones(3), None, fakes.ForwardMode("DECODE"), None)
 
 
-def test_swa_pool_rows_are_translated():
+def test_swa_pool_rows_need_the_device():
+    # the SWA table is translated by a HIP kernel; host tensors are refused, not served
     eng = _engine(swa=True)
     eng.alloc(1, 12)
     be = _backend(eng)
-    be.init_forward_metadata(eng.batch("DECODE", [1], new_tokens=[1]))
-    md = be.forward_metadata
-    want = eng.pool.full_to_swa_index_mapping[eng.req_to_token[1, :13].long()]
-    assert md.swa_table.shape == (1, 13)
-    assert md.swa_table[0].tolist() == want.tolist()
-    assert md.swa_row_index.tolist() == [0]
+    with pytest.raises(ValueError, match="device tensors"):
+        be.init_forward_metadata(eng.batch("DECODE", [1], new_tokens=[1]))
 
 
 @pytest.mark.parametrize("attr,value,reason", [

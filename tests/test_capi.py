@@ -153,3 +153,42 @@ def test_extend_workspace_covers_every_row_tile(lib):
     assert lib.ma_extend_workspace_bytes(1000, 40, 8, 3) == 256
     assert lib.ma_extend_workspace_bytes(100000, 64, 8, 300) == ((3125 + 300) * 8 + 255) // 256 * 256
     assert lib.ma_extend_workspace_bytes(10, 12, 8, 1) == 0
+
+
+@pytest.mark.parametrize("over,msg", [
+    ({"batch": -1}, ">= 0"),
+    ({"batch": 70000}, "65535"),
+    ({"ostride": 10, "width": 20}, "out_stride"),
+    ({"mapping": None}, "null pointer"),
+])
+def test_translate_slots_rejects_bad_arguments(lib, over, msg):
+    args = dict(table=1 << 20, tstride=64, rowidx=None, seq=1 << 21, batch=2, mapping=1 << 22, mlen=100,
+                out=1 << 23, ostride=64, width=64, stream=None)
+    args.update(over)
+    assert lib.ma_translate_slots(*args.values()) != 0
+    assert msg in lib.ma_last_error().decode()
+
+
+def test_translate_slots_of_nothing_is_a_no_op(lib):
+    assert lib.ma_translate_slots(None, 0, None, None, 0, None, 0, None, 0, 8, None) == 0
+
+
+def _g8_args(**over):
+    args = dict(k=1 << 20, v=1 << 21, sp=16 * 8 * 128, st=8 * 128, sh=128, dt=2, pages=10, table=1 << 22,
+                tstride=4, seq=1 << 23, batch=2, maxb=4, ps=16, hkv=8, dim=128, ko=1 << 24, vo=1 << 25,
+                stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("over,msg", [
+    ({"dt": 1}, "e4m3 or e5m2"),
+    ({"dim": 72}, "multiple of 16"),
+    ({"ps": 0}, "bad sizes"),
+    ({"ko": (1 << 24) + 8}, "aligned"),
+    ({"st": 1000}, "aligned"),
+    ({"tstride": 3}, "stride"),
+])
+def test_fp8_gather_rejects_bad_arguments(lib, over, msg):
+    assert lib.ma_gather_fp8_paged_kv(*_g8_args(**over)) != 0
+    assert msg in lib.ma_last_error().decode()
