@@ -18,7 +18,9 @@
 // head's K/V through its own L2.
 //
 // Per 64-key tile, per wave (scores of all 64 keys, then one online-softmax update, then
-// PV), MFMA 16x16x32 with fp32 accumulate:
+// PV), MFMA 16x16x32 with fp32 accumulate; the softmax's VALU work is what bounds the
+// kernel, so the row sums of P also come from an MFMA (a block of V^T whose row 0 is
+// ones) and the row max uses three-input maxima:
 //   S^T[key, row] = K[key, :] . Q[row, :]     A = K from LDS, B = Q^T (registers, whole kernel)
 //   O^T[d, row] += V^T[d, key] P^T[key, row]  A = V^T read transposed from LDS
 //                                             (ds_read_b64_tr_b16 / _tr_b8), B = P^T straight
@@ -295,12 +297,16 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   const int full_hi = a.causal ? min(seq, prefix + t_first + 1) : seq;
   const int ntiles = key_hi > key_lo ? (key_hi - key_lo + kXBN - 1) / kXBN : 0;
 
-  float m_run[kXRB], l_run[kXRB];
+  float m_run[kXRB];
   f32x4 o[kXRB][8];
+  // row sums of P, by MFMA: A = a 16 x 32 block whose row 0 is ones, so D[0][row] = sum_k P[row][k]
+  f32x4 lacc[kXRB];
+  const uint32_t one2 = (c == 0) ? 0x3C003C00u : 0u;
+  const u32x4 ones = u32x4{one2, one2, one2, one2};
 #pragma unroll
   for (int rb = 0; rb < kXRB; ++rb) {
     m_run[rb] = -INFINITY;
-    l_run[rb] = 0.f;
+    lacc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -308,6 +314,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   const unsigned char MA_GLOBAL* kbase = gptr(reinterpret_cast<const unsigned char*>(a.k));
   const unsigned char MA_GLOBAL* vbase = gptr(reinterpret_cast<const unsigned char*>(a.v));
   const int64_t row_bytes = a.kv_stride_row * kElt;
+  const uint32_t row_bytes32 = (uint32_t)row_bytes;  // the host checks it fits
   const int64_t head_off = (int64_t)h * a.kv_stride_head * kElt;
   auto swz = [](int t) -> int { return kFp8 ? ((t & 3) | ((t >> 2) & 4)) : ((2 * t) & 15); };
 
@@ -346,7 +353,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       vslot[x] = shfl_i(myslot, kFp8 ? (8 * xb + (lane >> 3)) : (4 * xb + (lane >> 4)));
     }
     // K: lane l -> key kb_w*16 + (l & 15), 16-byte chunk kKSub*j + sub
-    const unsigned char MA_GLOBAL* kp = kbase + (int64_t)kslot * row_bytes + head_off;
+    const unsigned char MA_GLOBAL* kp = kbase + (uint64_t)(uint32_t)kslot * row_bytes32 + head_off;
 #pragma unroll
     for (int x = 0; x < kKBlk; ++x) {
       const int blk = wave * kKBlk + x;
@@ -358,7 +365,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       const int xb = wave * kVBlk + x;
       const int tok = kFp8 ? (8 * xb + (lane >> 3)) : (4 * xb + (lane >> 4));
       const int pos = kFp8 ? (lane & 7) : (lane & 15);
-      dma(vbase + (int64_t)vslot[x] * row_bytes + head_off + ((pos ^ swz(tok)) << 4), vl + xb * 1024);
+      dma(vbase + (uint64_t)(uint32_t)vslot[x] * row_bytes32 + head_off + ((pos ^ swz(tok)) << 4), vl + xb * 1024);
     }
   };
   auto wait_vm = [&](auto N_) __attribute__((always_inline)) {
@@ -432,10 +439,20 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
             if (pos < lo_r[rb] || pos >= hi_r[rb]) s[rb][kb][i] = -INFINITY;
           }
       }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-        mx = fmaxf(mx, fmaxf(fmaxf(s[rb][kb][0], s[rb][kb][1]), fmaxf(s[rb][kb][2], s[rb][kb][3])));
+      // v_max3_f32 directly: scores come straight from the MFMAs, so the compiler
+      // would quiet them first (one extra v_max per value); there are no NaNs here
+      auto max3 = [](float x, float y, float z) __attribute__((always_inline)) {
+        float r;
+        __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
+        return r;
+      };
+      const f32x4* sr = s[rb];
+      const float m0 = max3(sr[0][0], sr[0][1], sr[0][2]);
+      const float m1 = max3(sr[0][3], sr[1][0], sr[1][1]);
+      const float m2 = max3(sr[1][2], sr[1][3], sr[2][0]);
+      const float m3 = max3(sr[2][1], sr[2][2], sr[2][3]);
+      const float m4 = max3(sr[3][0], sr[3][1], sr[3][2]);
+      float mx = max3(max3(m0, m1, m2), max3(m3, m4, sr[3][3]), -INFINITY);
       alpha[rb] = 1.f;
       if (__builtin_amdgcn_ballot_w64(mx > m_run[rb])) {
         mx = fmaxf(mx, shfl_xor_f(mx, 16));
@@ -453,10 +470,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[kb * 4 + i] = __builtin_amdgcn_exp2f(s[rb][kb][i] * a.scale_log2 - msc);
-      float ps = 0.f;
-#pragma unroll
-      for (int x = 0; x < 16; ++x) ps += p[x];
-      l_run[rb] = l_run[rb] * alpha[rb] + ps;
+
 #pragma unroll
       for (int st2 = 0; st2 < 2; ++st2)
 #pragma unroll
@@ -467,6 +481,8 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       for (int rb = 0; rb < kXRB; ++rb)
 #pragma unroll
         for (int db = 0; db < 8; ++db) o[rb][db] *= alpha[rb];
+#pragma unroll
+      for (int rb = 0; rb < kXRB; ++rb) lacc[rb] *= alpha[rb];
     }
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
@@ -494,6 +510,10 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
 #pragma unroll
         for (int rb = 0; rb < kXRB; ++rb) o[rb][db] = mfma16t<false>(va, pk[rb][hf], o[rb][db]);
       }
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int rb = 0; rb < kXRB; ++rb) lacc[rb] = mfma16t<false>(ones, pk[rb][hf], lacc[rb]);
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   };
 
@@ -549,9 +569,8 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   // ---- epilogue: normalise and write this lane's rows ----
 #pragma unroll
   for (int rb = 0; rb < kXRB; ++rb) {
-    float lt = l_run[rb];
-    lt += shfl_xor_f(lt, 16);
-    lt += shfl_xor_f(lt, 32);
+    // D[0][row] sits in element 0 of lane `row` (0..15)
+    const float lt = __builtin_bit_cast(float, shfl_i(__builtin_bit_cast(int, lacc[rb][0]), c));
     if (!real[rb]) continue;
     const int r = r0 + wave * (kXRB * 16) + rb * 16 + c;
     const int t = r / a.group;
@@ -621,6 +640,8 @@ extern "C" int ma_paged_extend(
        reinterpret_cast<uintptr_t>(out)) & 15)
     return set_error(MA_EINVAL, "q, k, v and out must be 16-byte aligned");
   const int elt = (kv_dtype >= DT_E4M3) ? 1 : 2;
+  if (kv_stride_row * elt >= ((int64_t)1 << 32))
+    return set_error(MA_EUNSUPPORTED, "KV row stride of %lld bytes exceeds 4 GiB", (long long)(kv_stride_row * elt));
   if (((kv_stride_row * elt) & 15) || ((kv_stride_head * elt) & 15) || ((q_stride_tok * 2) & 15) ||
       ((q_stride_head * 2) & 15) || ((out_stride_tok * 2) & 7) || ((out_stride_head * 2) & 7))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
