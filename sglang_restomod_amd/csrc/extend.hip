@@ -20,7 +20,8 @@
 // Per 64-key tile, per wave (scores of all 64 keys, then one online-softmax update, then
 // PV), MFMA 16x16x32 with fp32 accumulate; the softmax's VALU work is what bounds the
 // kernel, so the row sums of P also come from an MFMA (a block of V^T whose row 0 is
-// ones) and the row max uses three-input maxima:
+// ones), the row max uses three-input maxima, and O is rescaled only when a row's max
+// has grown by more than a factor 2^8 in p:
 //   S^T[key, row] = K[key, :] . Q[row, :]     A = K from LDS, B = Q^T (registers, whole kernel)
 //   O^T[d, row] += V^T[d, key] P^T[key, row]  A = V^T read transposed from LDS
 //                                             (ds_read_b64_tr_b16 / _tr_b8), B = P^T straight
@@ -53,6 +54,7 @@ constexpr int kXRB = 2;                        // 16-row blocks per wave
 constexpr int kXBM = kXWaves * kXRB * 16;      // query rows per workgroup
 constexpr int kXBN = 64;                       // keys per tile
 constexpr int kXD = 128;                       // head dim
+constexpr float kLazyRescale = 8.f;            // log2 of the largest p between rescales
 
 // One entry of the work list: sequence in the low 32 bits, row tile in the high 32;
 // -1 (sequence -1) past the last tile.
@@ -454,7 +456,10 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       const float m4 = max3(sr[3][0], sr[3][1], sr[3][2]);
       float mx = max3(max3(m0, m1, m2), max3(m3, m4, sr[3][3]), -INFINITY);
       alpha[rb] = 1.f;
-      if (__builtin_amdgcn_ballot_w64(mx > m_run[rb])) {
+      // the exponent base only moves when some row's max has grown by more than
+      // 2^kLazyRescale in p: until then p stays <= 2^kLazyRescale (exact in fp16's
+      // relative precision, fp32 sums) and O is not rescaled
+      if (__builtin_amdgcn_ballot_w64((mx - m_run[rb]) * a.scale_log2 > kLazyRescale)) {
         mx = fmaxf(mx, shfl_xor_f(mx, 16));
         mx = fmaxf(mx, shfl_xor_f(mx, 32));
         const float m_new = fmaxf(m_run[rb], mx);
