@@ -75,6 +75,22 @@ __device__ __forceinline__ f32x4 mfma16t(const u32x4& a, const u32x4& b, f32x4 c
 }
 
 // ---------------------------------------------------------------------------
+// Online softmax helpers.
+// ---------------------------------------------------------------------------
+// A row's exponent base moves only when its max has grown by more than this (log2 of the
+// largest p between two rescales of O). p stays exact to fp16's relative precision and
+// the sums are fp32, so the result is the same up to rounding; O is rescaled rarely.
+constexpr float kLazyRescale = 8.f;
+
+// Max of three floats as one v_max3_f32. Scores come straight from MFMAs, which the
+// compiler would quiet first (one more v_max per value) before fmaxf; scores hold no NaN.
+__device__ __forceinline__ float max3f(float x, float y, float z) {
+  float r;
+  __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
+  return r;
+}
+
+// ---------------------------------------------------------------------------
 // fp8 -> 16-bit, two values per instruction (exact: every e4m3fn / e5m2 value is
 // representable in both fp16 and bf16). `w` holds four fp8 bytes; `hi` selects
 // bytes 2..3 instead of 0..1. Result: low half = first byte, high half = second.

@@ -54,7 +54,6 @@ constexpr int kXRB = 2;                        // 16-row blocks per wave
 constexpr int kXBM = kXWaves * kXRB * 16;      // query rows per workgroup
 constexpr int kXBN = 64;                       // keys per tile
 constexpr int kXD = 128;                       // head dim
-constexpr float kLazyRescale = 8.f;            // log2 of the largest p between rescales
 
 // One entry of the work list: sequence in the low 32 bits, row tile in the high 32;
 // -1 (sequence -1) past the last tile.
@@ -441,20 +440,13 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
             if (pos < lo_r[rb] || pos >= hi_r[rb]) s[rb][kb][i] = -INFINITY;
           }
       }
-      // v_max3_f32 directly: scores come straight from the MFMAs, so the compiler
-      // would quiet them first (one extra v_max per value); there are no NaNs here
-      auto max3 = [](float x, float y, float z) __attribute__((always_inline)) {
-        float r;
-        __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
-        return r;
-      };
       const f32x4* sr = s[rb];
-      const float m0 = max3(sr[0][0], sr[0][1], sr[0][2]);
-      const float m1 = max3(sr[0][3], sr[1][0], sr[1][1]);
-      const float m2 = max3(sr[1][2], sr[1][3], sr[2][0]);
-      const float m3 = max3(sr[2][1], sr[2][2], sr[2][3]);
-      const float m4 = max3(sr[3][0], sr[3][1], sr[3][2]);
-      float mx = max3(max3(m0, m1, m2), max3(m3, m4, sr[3][3]), -INFINITY);
+      const float m0 = max3f(sr[0][0], sr[0][1], sr[0][2]);
+      const float m1 = max3f(sr[0][3], sr[1][0], sr[1][1]);
+      const float m2 = max3f(sr[1][2], sr[1][3], sr[2][0]);
+      const float m3 = max3f(sr[2][1], sr[2][2], sr[2][3]);
+      const float m4 = max3f(sr[3][0], sr[3][1], sr[3][2]);
+      float mx = max3f(max3f(m0, m1, m2), max3f(m3, m4, sr[3][3]), -INFINITY);
       alpha[rb] = 1.f;
       // the exponent base only moves when some row's max has grown by more than
       // 2^kLazyRescale in p: until then p stays <= 2^kLazyRescale (exact in fp16's

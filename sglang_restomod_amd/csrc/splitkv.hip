@@ -527,16 +527,23 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
             if (pos < lo_r[nb] || pos >= hi_r[nb]) s[nb][tb][i] = -INFINITY;
           }
       }
-      float mx = fmaxf(fmaxf(fmaxf(s[nb][0][0], s[nb][0][1]), fmaxf(s[nb][0][2], s[nb][0][3])),
-                       fmaxf(fmaxf(s[nb][1][0], s[nb][1][1]), fmaxf(s[nb][1][2], s[nb][1][3])));
-      mx = fmaxf(mx, shfl_xor_f(mx, 16));
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
-      const float m_new = fmaxf(m_run[nb], mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      grew |= (m_new != m_run[nb]);
-      alpha[nb] = __builtin_amdgcn_exp2f((m_run[nb] - m_use) * a.scale_log2);
-      m_run[nb] = m_new;
-      const float msc = m_use * a.scale_log2;
+      const f32x4* sr = s[nb];
+      float mx = max3f(max3f(sr[0][0], sr[0][1], sr[0][2]), max3f(sr[0][3], sr[1][0], sr[1][1]),
+                       max3f(sr[1][2], sr[1][3], -INFINITY));
+      alpha[nb] = 1.f;
+      // fp8 KV (more VALU per tile for the conversions): the exponent base moves only when
+      // some row's max has grown by more than 2^kLazyRescale in p, so the cross-lane max
+      // and the rescale of O are rare. 16-bit KV measured faster with the update each tile.
+      if (!kFp8 || __builtin_amdgcn_ballot_w64((mx - m_run[nb]) * a.scale_log2 > kLazyRescale)) {
+        mx = fmaxf(mx, shfl_xor_f(mx, 16));
+        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        const float m_new = fmaxf(m_run[nb], mx);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        grew |= (m_new != m_run[nb]);
+        alpha[nb] = __builtin_amdgcn_exp2f((m_run[nb] - m_use) * a.scale_log2);
+        m_run[nb] = m_new;
+      }
+      const float msc = ((m_run[nb] == -INFINITY) ? 0.f : m_run[nb]) * a.scale_log2;
       float p[8];
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb)
