@@ -110,8 +110,9 @@ __device__ __forceinline__ uint32_t cvt2_fp8(uint32_t w, bool hi) {
       if (hi) return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, true));
       return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, false));
     } else {
-      if (hi) return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true));
-      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false));
+      // e5m2 is the high byte of the fp16 with the same value: one byte permute
+      // (selector 0x0c gives a zero byte)
+      return __builtin_amdgcn_perm(0u, w, hi ? 0x030c020cu : 0x010c000cu);
     }
   }
 }

@@ -36,15 +36,11 @@ struct Fp8GatherArgs {
   uint16_t* v_out;
 };
 
+// 8 fp8 bytes -> 8 fp16 values (cvt8_fp8: e5m2 by byte permute, e4m3fn by the hardware
+// conversion)
 template <int KV>
 __device__ __forceinline__ u32x4 decode8(uint32_t w0, uint32_t w1) {
-  if constexpr (KV == DT_E5M2) {
-    // byte i -> (byte << 8): v_perm places each byte in the high half of a 16-bit lane
-    return u32x4{perm(0u, w0, 0x010c000cu), perm(0u, w0, 0x030c020cu), perm(0u, w1, 0x010c000cu),
-                 perm(0u, w1, 0x030c020cu)};
-  } else {
-    return cvt8_fp8<KV, false>(w0, w1);
-  }
+  return cvt8_fp8<KV, false>(w0, w1);
 }
 
 template <int KV>
