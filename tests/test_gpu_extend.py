@@ -198,3 +198,57 @@ def test_extend_work_list_lists_every_row_tile_heaviest_first(gpu):
 
     costs = [key_tiles(b, rt) for b, rt in listed]
     assert costs == sorted(costs, reverse=True)
+
+
+def test_extend_in_a_hip_graph_replays_new_splits():
+    """A captured extend (fixed token count and batch) replays correctly when the split of
+    the tokens across sequences and the prefixes change: the work list is rebuilt on the
+    device at every replay."""
+    heads, heads_kv, T = 40, 8, 300
+    splits = [([10, 0, 77], [100, 150, 50]), ([400, 5, 0], [1, 298, 1]), ([0, 0, 0], [300, 0, 0])]
+    prefix0, extend0 = splits[0]
+    # one pool large enough for every split
+    gpu_dev = torch.device("cuda:0")
+    q, k, v, table, _, _ = _synthetic(gpu_dev, [700, 700, 700], [300, 300, 300],
+                                      heads, heads_kv)
+    ops = _ops()
+    B = 3
+    qs = torch.randn(T, heads, 128, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(gpu_dev)
+    seq_b = torch.zeros(B, dtype=torch.int32, device=gpu_dev)
+    qsl_b = torch.zeros(B + 1, dtype=torch.int32, device=gpu_dev)
+    pre_b = torch.zeros(B, dtype=torch.int32, device=gpu_dev)
+    ws = ops.extend_workspace(gpu_dev, T, heads, heads_kv, B)
+    out = torch.empty_like(qs)
+    tab = table.to(gpu_dev)
+
+    def load(prefix, extend):
+        seq_b.copy_(torch.tensor([p + e for p, e in zip(prefix, extend)], dtype=torch.int32))
+        qsl_b.copy_(torch.tensor([0, extend[0], extend[0] + extend[1], sum(extend)], dtype=torch.int32))
+        pre_b.copy_(torch.tensor(prefix, dtype=torch.int32))
+
+    def run():
+        ops.paged_extend_forward(qs, k, v, tab, seq_b, qsl_b, pre_b, softmax_scale=128 ** -0.5, out=out,
+                                 workspace=ws)
+
+    load(prefix0, extend0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    t = table.numpy()
+    for it, (prefix, extend) in enumerate(splits * 2):
+        load(prefix, extend)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        run()
+        torch.cuda.synchronize()
+        assert torch.equal(got, out), f"replay {it} differs from the eager call"
+        qsl = [0, extend[0], extend[0] + extend[1], sum(extend)]
+        rows_of = {b: list(range(extend[b])) for b in range(B)}
+        _check_rows(qs, k, v, lambda b, n: oracle.slots_from_page_table(t, b, n, 1), prefix, qsl, got,
+                    rows_of, 128 ** -0.5, what=f"replay {it}")
