@@ -247,3 +247,35 @@ def test_verify_ragged_query_counts(gpu):
     ref = oracle.paged_attention(to_f64(q), to_f64(k), to_f64(v), [table[b].numpy() for b in range(B)],
                                  qsl.tolist(), prefix, seq, softmax_scale=D ** -0.5)
     assert_attn_close(out, ref, what="ragged verify")
+
+
+@pytest.mark.parametrize("mode", ["decode", "verify"])
+def test_poisoned_workspace_and_output(gpu, mode):
+    """The workspace needs no initialisation: filled with 0xFF bytes (NaN pieces, -1
+    descriptors) and reused by a smaller call, and with the output pre-filled with NaN,
+    every result is the one a fresh workspace gives, bit for bit."""
+    ops = _ops()
+    idx = 1 if mode == "decode" else 4
+    big = workloads.make(idx, device=gpu, batch=12, scale_lens=0.3)
+    small = workloads.make(idx, device=gpu, batch=3, scale_lens=0.05)
+
+    def run(w, ws, out):
+        if mode == "decode":
+            return ops.grouped_decode_forward(
+                w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, softmax_scale=w.softmax_scale,
+                row_index=w.req_pool_indices, out=out, workspace=ws)
+        T = int(w.extend_lens[0])
+        return ops.paged_verify_forward(
+            w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, w.query_start_loc, w.prefix_lens,
+            max_q_per_seq=T, softmax_scale=w.softmax_scale, out=out, row_index=w.req_pool_indices,
+            workspace=ws)
+
+    fresh = ops.splitkv_workspace(torch.device(gpu))
+    want = [run(w, fresh, None).clone() for w in (big, small)]
+    poisoned = ops.splitkv_workspace(torch.device(gpu))
+    poisoned.fill_(0xFF)
+    for w, ref in zip((big, small), want):   # the small call sees the big call's leftovers
+        out = torch.full_like(ref, float("nan"))
+        run(w, poisoned, out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"{mode}: a poisoned or stale workspace changed the result"
