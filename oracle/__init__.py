@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the shipped package imports this
 directory: only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
-``cpu_baseline`` leg may use it, and only as the checker (or, for the CPU
+``cpu_baseline`` leg may use it, and only to check results (or, for the CPU
 baseline, as the timed torch-native restatement). The product path raises when
 its HIP library is missing; it never falls back to anything here.
 
@@ -17,6 +17,8 @@ Modules
                   CPU baseline.
 ``fp8``           bit-level decoding of OCP e4m3fn / e5m2 bytes.
 ``metadata``      page-table / query-start / verify-row metadata construction.
+``kv_write``      the token pool's write with quantisation on write (divide in the
+                  source dtype, round to nearest even onto the fp8 grid).
 
 The seeded generators of the five benchmark workloads are not part of the oracle:
 they live in ``sglang_restomod_amd/workloads.py``.
