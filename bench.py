@@ -76,10 +76,7 @@ def _calibrate_copy(mib):
                       "GBps_read_plus_write": 2 * n / dt / 1e9}))
 
 
-GATHER_ORDERS = {0: "random slots, head-major", 1: "random slots, head-minor", 2: "in order"}
-
-
-def _gather_ceiling(num_tokens, heads, row_bytes, order, steps=20):
+def _gather_ceiling(num_tokens, heads, row_bytes, steps=20):
     """Read bandwidth of a plain gather of ``num_tokens * heads`` rows of ``row_bytes``
     (libma_calibrate.so, csrc/calibrate/gather_ceiling.hip): the attainable rate of the
     KV access pattern without any attention arithmetic. Returns GB/s."""
@@ -89,23 +86,23 @@ def _gather_ceiling(num_tokens, heads, row_bytes, order, steps=20):
 
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "sglang_restomod_amd", "libma_calibrate.so")
     lib = ctypes.CDLL(path)
-    lib.ma_gather_ceiling_blocks.restype = ctypes.c_int64
-    lib.ma_gather_ceiling_blocks.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.ma_gather_ceiling_sink_words.restype = ctypes.c_int64
+    lib.ma_gather_ceiling_sink_words.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int]
     lib.ma_gather_ceiling.restype = ctypes.c_int
     lib.ma_gather_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
-                                      ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+                                      ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(0)
     pool = torch.randint(0, 256, (num_tokens * heads * row_bytes,), dtype=torch.uint8, device=dev, generator=g)
     perm = torch.randperm(num_tokens, device=dev, generator=g).to(torch.int32)
-    rows_per_wave = 64
-    blocks = lib.ma_gather_ceiling_blocks(num_tokens, heads, row_bytes, rows_per_wave)
-    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    chunks_per_wave = 4
+    sink = torch.empty(lib.ma_gather_ceiling_sink_words(num_tokens, heads, chunks_per_wave), dtype=torch.int32,
+                       device=dev)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
     def run():
-        rc = lib.ma_gather_ceiling(pool.data_ptr(), perm.data_ptr(), num_tokens, heads, row_bytes, order,
-                                   rows_per_wave, sink.data_ptr(), sink.numel(), stream)
+        rc = lib.ma_gather_ceiling(pool.data_ptr(), perm.data_ptr(), num_tokens, heads, row_bytes,
+                                   chunks_per_wave, sink.data_ptr(), sink.numel(), stream)
         if rc != 0:
             raise RuntimeError(f"ma_gather_ceiling failed ({rc})")
 
@@ -306,7 +303,7 @@ def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
         # the same number of K and V rows, gathered from random slots with no arithmetic
         row_bytes = w.dim * w.k_pool.element_size()
         tokens = 2 * int(sum(w.seq_lens_cpu))
-        res["gather_ceiling_GBps"] = _gather_ceiling(tokens, w.heads_kv, row_bytes, 0)
+        res["gather_ceiling_GBps"] = _gather_ceiling(tokens, w.heads_kv, row_bytes)
         res["gather_row_bytes"] = row_bytes
     if cpu_baseline:
         med, frac, cores, rows = _cpu_baseline(w, cpu_seconds)
