@@ -53,6 +53,8 @@ def _parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", type=int, default=1)
+    p.add_argument("--kv-format", choices=("e4m3", "e5m2"), default="e4m3",
+                   help="fp8 format of workload 3's KV")
     p.add_argument("--secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -333,7 +335,8 @@ def main():
     if args.calibrate_copy:
         _calibrate_copy(args.calibrate_copy)
         return
-    head = _measure(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_seconds)
+    head = _measure(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_seconds,
+                    kv_format=args.kv_format)
     bound_hbm = head["mode"] != "extend"
     kernel = "splitkv_partial" if bound_hbm else "extend_kernel"
     line = {
