@@ -1,0 +1,136 @@
+"""A seeded sweep of random shapes through all three kernels against the float64 oracle.
+
+Each case draws a batch of ragged sequences (empty ones included), a GQA ratio, a KV
+dtype (bf16, fp16, e4m3fn or e5m2 with scales), causal or not, and a sliding window or
+none. Slots are a random permutation of a shared pool, and the table rows are
+permuted inside a larger ``req_to_token``. The same case runs through the split-KV
+decode (the last token of each sequence), the split-KV verify (up to 16 rows per
+sequence) and the MFMA extend (any number of rows). The sizes keep the oracle fast.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oracle
+from tests.helpers import assert_attn_close, to_f64
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+KV = [torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float8_e5m2]
+
+
+def _ops():
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    return ops
+
+
+def _case(seed, max_q):
+    g = np.random.default_rng(seed)
+    B = int(g.integers(1, 7))
+    hkv = int(g.choice([1, 2, 4, 8]))
+    G = int(g.choice([1, 2, 3, 5, 8]))
+    kv = KV[int(g.integers(0, len(KV)))]
+    q_dtype = torch.float16 if kv == torch.float16 else (torch.bfloat16 if kv == torch.bfloat16 else
+                                                         (torch.float16 if g.random() < 0.3 else torch.bfloat16))
+    prefix = [int(x) for x in g.integers(0, 700, B)]
+    ext = [int(x) for x in g.integers(0, max_q + 1, B)]
+    if sum(ext) == 0:
+        ext[0] = 1
+    causal = bool(g.random() < 0.8)
+    window = int(g.choice([-1, -1, 0, 17, 100]))
+    k_scale, v_scale = (float(g.uniform(0.5, 2)), float(g.uniform(0.5, 2))) if kv in KV[2:] else (1.0, 1.0)
+    return B, hkv, G, kv, q_dtype, prefix, ext, causal, window, k_scale, v_scale
+
+
+def _build(seed, max_q):
+    B, hkv, G, kv, q_dtype, prefix, ext, causal, window, ks, vs = _case(seed, max_q)
+    gen = torch.Generator().manual_seed(seed)
+    seq = [p + e for p, e in zip(prefix, ext)]
+    pool = sum(seq) + 64
+    kf = torch.randn(pool, hkv, 128, generator=gen)
+    vf = torch.randn(pool, hkv, 128, generator=gen)
+    if kv in KV[2:]:
+        k = (kf / ks).to(kv)
+        v = (vf / vs).to(kv)
+    else:
+        k, v = kf.to(kv), vf.to(kv)
+    T = sum(ext)
+    q = torch.randn(T, hkv * G, 128, generator=gen).to(q_dtype)
+    perm = torch.randperm(pool - 1, generator=gen) + 1
+    rows = torch.randperm(B + 3, generator=gen)[:B]
+    r2t = torch.zeros(B + 3, max(seq) + 5, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(seq):
+        r2t[rows[b], :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    qsl = [0] + list(np.cumsum(ext))
+    case = dict(q=q, k=k, v=v, r2t=r2t, rows=rows, seq=seq, prefix=prefix, ext=ext, qsl=qsl, causal=causal,
+                window=window, ks=ks, vs=vs, scale=128 ** -0.5)
+    print(f"[case] seed={seed} B={B} hkv={hkv} G={G} kv={kv} q={q_dtype} prefix={prefix} ext={ext} "
+          f"causal={causal} window={window}", flush=True)
+    return case
+
+
+def _reference(c):
+    kp = c["k"].float().numpy().astype(np.float64)
+    vp = c["v"].float().numpy().astype(np.float64)
+    slots = [c["r2t"][int(c["rows"][b]), :n].numpy().astype(np.int64) for b, n in enumerate(c["seq"])]
+    return oracle.paged_attention(to_f64(c["q"]), kp, vp, slots, c["qsl"], c["prefix"], c["seq"],
+                                  softmax_scale=c["scale"], k_scale=c["ks"], v_scale=c["vs"], causal=c["causal"],
+                                  sliding_window=c["window"])
+
+
+def _device(c):
+    d = {n: c[n].to(DEV) for n in ("q", "k", "v", "r2t")}
+    d["rows"] = c["rows"].to(torch.int64).to(DEV)
+    d["seq"] = torch.tensor(c["seq"], dtype=torch.int32, device=DEV)
+    d["qsl"] = torch.tensor(c["qsl"], dtype=torch.int32, device=DEV)
+    d["pre"] = torch.tensor(c["prefix"], dtype=torch.int32, device=DEV)
+    return d
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_extend(seed):
+    c = _build(1000 + seed, max_q=200)
+    d = _device(c)
+    out = _ops().paged_extend_forward(
+        d["q"], d["k"], d["v"], d["r2t"], d["seq"], d["qsl"], d["pre"], softmax_scale=c["scale"],
+        k_scale=c["ks"], v_scale=c["vs"], causal=c["causal"], sliding_window_size=c["window"], row_index=d["rows"])
+    torch.cuda.synchronize()
+    assert_attn_close(out, _reference(c), what=f"extend seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_verify(seed):
+    c = _build(2000 + seed, max_q=16)
+    d = _device(c)
+    out = _ops().paged_verify_forward(
+        d["q"], d["k"], d["v"], d["r2t"], d["seq"], d["qsl"], d["pre"], max_q_per_seq=max(max(c["ext"]), 1),
+        softmax_scale=c["scale"], k_scale=c["ks"], v_scale=c["vs"], causal=c["causal"],
+        sliding_window_size=c["window"], row_index=d["rows"])
+    torch.cuda.synchronize()
+    assert_attn_close(out, _reference(c), what=f"verify seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_decode(seed):
+    c = _build(3000 + seed, max_q=1)
+    # one query row per sequence, at its last position; empty sequences return zeros
+    ctx = c["seq"]
+    B, hq = len(ctx), c["q"].shape[1]
+    gen = torch.Generator().manual_seed(3000 + seed)
+    c["q"] = torch.randn(B, hq, 128, generator=gen).to(c["q"].dtype)
+    c["qsl"] = list(range(B + 1))
+    c["prefix"] = [max(n - 1, 0) for n in ctx]
+    c["causal"] = True
+    d = _device(c)
+    out = _ops().grouped_decode_forward(
+        d["q"], d["k"], d["v"], d["r2t"], d["seq"], softmax_scale=c["scale"], k_scale=c["ks"], v_scale=c["vs"],
+        row_index=d["rows"], sliding_window_size=c["window"])
+    torch.cuda.synchronize()
+    assert_attn_close(out, _reference(c), what=f"decode seed {seed}")
