@@ -279,3 +279,34 @@ def test_poisoned_workspace_and_output(gpu, mode):
         run(w, poisoned, out)
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"{mode}: a poisoned or stale workspace changed the result"
+
+
+def test_two_streams_with_their_own_workspaces(gpu):
+    """Calls that overlap in time on two streams, each with the shared workspace of its
+    own stream, give the results of the same calls run one after another."""
+    ops = _ops()
+    w1 = workloads.make(1, device=gpu, batch=16, scale_lens=0.4)
+    w2 = workloads.make(4, device=gpu, batch=8, scale_lens=0.3)
+
+    def dec(out=None):
+        return ops.grouped_decode_forward(w1.q, w1.k_pool, w1.v_pool, w1.req_to_token, w1.seq_lens,
+                                          softmax_scale=w1.softmax_scale, row_index=w1.req_pool_indices, out=out)
+
+    def ver(out=None):
+        return ops.paged_verify_forward(w2.q, w2.k_pool, w2.v_pool, w2.req_to_token, w2.seq_lens,
+                                        w2.query_start_loc, w2.prefix_lens, max_q_per_seq=4,
+                                        softmax_scale=w2.softmax_scale, row_index=w2.req_pool_indices, out=out)
+
+    want1, want2 = dec().clone(), ver().clone()
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    o1, o2 = torch.empty_like(want1), torch.empty_like(want2)
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    for _ in range(5):
+        with torch.cuda.stream(s1):
+            dec(o1)
+        with torch.cuda.stream(s2):
+            ver(o2)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, want1) and torch.equal(o2, want2)
