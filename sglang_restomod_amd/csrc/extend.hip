@@ -385,14 +385,14 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
         v[w] = pack_f16(__builtin_bit_cast(float, v[w] << 16), __builtin_bit_cast(float, v[w] & 0xffff0000u));
       *pv = v;
     }
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   };
   // per-lane part of the V^T read addresses (16-bit V): row 4j + e, column bits of cc
   const int vrow = (4 * j + (c >> 2)) * kRowB + ((lane & 3) >> 1) * 16 + (lane & 1) * 8;
   const int vs1 = (4 * j + (c >> 2)) & 7;
 
-  // ---- one tile: scores for all 64 keys, one softmax update, PV ----
-  auto compute = [&](int tile, int st) __attribute__((always_inline)) {
+  // ---- one tile: scores for all 64 keys, then mid() (work that overlaps the score
+  // MFMAs), one softmax update, PV ----
+  auto compute = [&](int tile, int st, auto&& mid) __attribute__((always_inline)) {
     const unsigned char* kt = kring[st];
     const unsigned char* vt = vring[st];
     const int base = key_lo + tile * kXBN;
@@ -425,6 +425,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
           for (int rb = 0; rb < kXRB; ++rb) s[rb][kb] = mfma16t<QBF16>(kf, qv[rb][kk], s[rb][kb]);
         }
     }
+    mid();
     const bool full = (base >= full_lo) && (base + kXBN <= full_hi);
     u32x4 pk[kXRB][2];
     float alpha[kXRB];
@@ -511,14 +512,14 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int rb = 0; rb < kXRB; ++rb) lacc[rb] = mfma16t<false>(ones, pk[rb][hf], lacc[rb]);
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   };
 
   // ---- schedule ----
   // Step k: look up the slots of tile k+A; once the slots of tile k+S-1 (looked up at
   // step k-2) have landed, and at k >= 0 after a barrier, issue tile k+S-1 into stage
-  // (k+S-1) % S; at k >= 0 compute tile k from stage k % S. Steps -A..-1 are the
-  // prologue. Instructions issued per step: one slot lookup, plus ND from step 1-S on.
+  // (k+S-1) % S; at k >= 0 compute tile k from stage k % S, converting tile k+1's bf16 V
+  // while the scores' MFMAs run. Steps -A..-1 are the prologue. Instructions issued per
+  // step: one slot lookup, plus ND from step 1-S on.
   auto nd_at = [](int k) constexpr -> int { return k >= 1 - S ? ND : 0; };
   auto wait_at = [nd_at](int k) constexpr -> int {  // issued after the slot lookup of step k-2
     int n = 0;
@@ -540,15 +541,21 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       if (k >= 0) barrier();
       issue(slot_of(k + S - 1, sreg[DI]), DI);
     }
-    if constexpr (kConvV) {
-      // tile k+1 (issued at step k+2-S) has landed once at most (S-2)*OPS newer
-      // instructions (those of steps k+3-S .. k) remain
-      if (k >= -1) {
-        wait_vm(std::integral_constant<int, (S - 2) * OPS>{});
-        convert_v(((KC + 1) % S + S) % S);
+    // bf16 V of tile k+1 -> fp16, inside tile k's compute after its score MFMAs are
+    // issued (or on its own where no tile is computed); its LDS writes are waited for
+    // before the next barrier. Tile k+1 (issued at step k+2-S) has landed once at most
+    // (S-2)*OPS newer instructions (those of steps k+3-S .. k) remain.
+    auto conv = [&]() __attribute__((always_inline)) {
+      if constexpr (kConvV) {
+        if (k >= -1) {
+          wait_vm(std::integral_constant<int, (S - 2) * OPS>{});
+          convert_v(((KC + 1) % S + S) % S);
+        }
       }
-    }
-    if (k >= 0 && k < ntiles) compute(k, ((KC % S) + S) % S);
+    };
+    if (k >= 0 && k < ntiles) compute(k, ((KC % S) + S) % S, conv);
+    else conv();
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   };
 
   if (ntiles > 0) {
