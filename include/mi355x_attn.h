@@ -25,6 +25,11 @@
  * Score scale is softmax_scale * k_scale; outputs are multiplied by v_scale
  * (sglang_restomod/attention/v100/tilelang/_paged_adapter.py:658,753-754).
  * Query head h reads kv head h / (num_q_heads / num_kv_heads).
+ *
+ * Head dims of the attention entry points: 64, 128 or 256 (the reference's paged
+ * kernels have configurations for 64, 128, 256 and 512, _kernels_paged.py:398-410).
+ * fp8 pools at head_dim 64 are read by the split-KV calls only; ma_paged_extend
+ * refuses them. Other head dims return MA_EUNSUPPORTED.
  */
 #ifndef MI355X_ATTN_H
 #define MI355X_ATTN_H
@@ -36,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 6
+#define MA_ABI_VERSION 7
 
 /* dtype codes */
 #define MA_DT_F16 0
@@ -125,9 +130,10 @@ int ma_paged_verify(const void* q, int64_t q_stride_tok, int64_t q_stride_head, 
 
 /*
  * Bytes of workspace ma_paged_extend needs for `num_tokens` query tokens in `batch`
- * sequences: the work list, one 8-byte entry per 256-row tile (at most
- * ceil(num_tokens * G / 256) + batch, G = num_q_heads / num_kv_heads). 0 for bad
- * arguments.
+ * sequences: the work list, one 8-byte entry per row tile. Row tiles have 256 rows at
+ * head_dim 64 and 128 and 128 rows at 256; the size covers the smaller tile (at most
+ * ceil(num_tokens * G / 128) + batch entries, G = num_q_heads / num_kv_heads), so one
+ * workspace serves every head dim. 0 for bad arguments.
  */
 size_t ma_extend_workspace_bytes(int64_t num_tokens, int num_q_heads, int num_kv_heads, int batch);
 

@@ -18,7 +18,7 @@ from .backend_registry import env_flag
 
 ENV_FLAG = "SGLANG_MI355X_DRAFT_DECODE_NATIVE"
 PAGE_SIZE = 1
-SUPPORTED_HEAD_DIMS = (128,)  # the kernels' head_dim (ops.SUPPORTED_HEAD_DIMS)
+SUPPORTED_HEAD_DIMS = (64, 128, 256)  # the kernels' head dims (ops.SUPPORTED_HEAD_DIMS)
 
 
 def native_enabled(env: Mapping[str, str] | None = None) -> bool:

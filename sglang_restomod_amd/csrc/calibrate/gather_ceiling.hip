@@ -1,13 +1,13 @@
 // Measurement kernel (not part of the attention library): the HBM read bandwidth of
 // gathering rows of a token pool [num_tokens, heads, row_bytes] from random slots, with
 // no arithmetic. It gives an attainable rate for the KV access pattern of paged decode
-// with page size 1: rows of one kv head (256 B for D=128 in 16 bits, 128 B in fp8) at
+// with page size 1: rows of one kv head (64 to 512 B: D=128 in 16 bits is 256 B) at
 // random pool slots, each row read once per kv head, in the decode's head-major order.
 //
 // Workgroup (x, h): 4 waves; a wave reads the rows of head h for chunks_per_wave chunks of
 // 64 consecutive entries of `perm` (its slots). Each lane loads one slot per chunk, and
 // the rows of each 1 KB load instruction take their slots by ds_bpermute, so the row
-// loads of a chunk (16 x 1 KB for 256 B rows, 8 for 128 B) are in flight together while
+// loads of a chunk (row_bytes / 16 loads of 1 KB) are in flight together while
 // the next chunk's slots load. The XOR of everything read goes to one word per thread.
 
 #include <hip/hip_runtime.h>
@@ -73,11 +73,17 @@ extern "C" int ma_gather_ceiling(const void* pool, const int32_t* perm, int64_t 
   const dim3 grid((unsigned)bx, (unsigned)heads);
   const unsigned char* p = reinterpret_cast<const unsigned char*>(pool);
   hipStream_t st = (hipStream_t)stream;
-  if (row_bytes == 256)
+  if (row_bytes == 512)
+    hipLaunchKernelGGL(gather_ceiling_kernel<512>, grid, dim3(kThreads), 0, st, p, perm, num_tokens, heads,
+                       chunks_per_wave, sink);
+  else if (row_bytes == 256)
     hipLaunchKernelGGL(gather_ceiling_kernel<256>, grid, dim3(kThreads), 0, st, p, perm, num_tokens, heads,
                        chunks_per_wave, sink);
   else if (row_bytes == 128)
     hipLaunchKernelGGL(gather_ceiling_kernel<128>, grid, dim3(kThreads), 0, st, p, perm, num_tokens, heads,
+                       chunks_per_wave, sink);
+  else if (row_bytes == 64)
+    hipLaunchKernelGGL(gather_ceiling_kernel<64>, grid, dim3(kThreads), 0, st, p, perm, num_tokens, heads,
                        chunks_per_wave, sink);
   else
     return -1;

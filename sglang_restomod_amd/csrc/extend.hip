@@ -49,11 +49,18 @@
 
 namespace ma {
 
-constexpr int kXWaves = 8;                     // waves per workgroup
-constexpr int kXRB = 2;                        // 16-row blocks per wave
-constexpr int kXBM = kXWaves * kXRB * 16;      // query rows per workgroup
-constexpr int kXBN = 64;                       // keys per tile
-constexpr int kXD = 128;                       // head dim
+constexpr int kXWaves = 8;  // waves per workgroup
+
+// Tile shape per head dim (64, 128 or 256). Q and O take registers in proportion to the
+// head dim, so at D = 256 a wave holds one 16-row block and a tile has 32 keys; the K
+// and V stages keep their size in LDS.
+template <int D>
+struct XShape {
+  static constexpr int BN = D == 256 ? 32 : 64;  // keys per tile
+  static constexpr int RB = D == 256 ? 1 : 2;    // 16-row blocks per wave
+  static constexpr int BM = kXWaves * RB * 16;   // query rows per workgroup
+};
+constexpr int kXBMMin = XShape<256>::BM;  // the smallest row tile: it sizes the work list
 
 // One entry of the work list: sequence in the low 32 bits, row tile in the high 32;
 // -1 (sequence -1) past the last tile.
@@ -81,14 +88,14 @@ struct ExtendArgs {
   int64_t out_stride_tok, out_stride_head;
 };
 
-// Keys [lo, hi) that some row of the row tile starting at row r0 of a sequence may see.
+// Keys [lo, hi) that some row of the bm-row tile starting at row r0 of a sequence may see.
 struct KeyRange {
   int lo, hi;
 };
-__device__ __forceinline__ KeyRange row_tile_keys(int r0, int ntok, int group, int prefix, int seq, int causal,
-                                                  int window) {
+__device__ __forceinline__ KeyRange row_tile_keys(int r0, int bm, int ntok, int group, int prefix, int seq,
+                                                  int causal, int window) {
   const int t_first = r0 / group;
-  const int t_last = min(ntok - 1, (r0 + kXBM - 1) / group);
+  const int t_last = min(ntok - 1, (r0 + bm - 1) / group);
   KeyRange k;
   k.lo = window >= 0 ? max(0, prefix + t_first - window) : 0;
   k.hi = causal ? min(seq, prefix + t_last + 1) : seq;
@@ -106,13 +113,14 @@ struct ExtendPlanArgs {
   const int32_t* seq_lens;
   const int32_t* prefix;
   int batch, group, causal, window;
-  int capacity;  // entries of items
+  int tile_rows, tile_keys;  // the extend kernel's rows per workgroup and keys per tile
+  int capacity;              // entries of items
   int64_t* items;
 };
 
-// Row tiles of a sequence with ntok query tokens.
-__device__ __forceinline__ int seq_row_tiles(int ntok, int group) {
-  return ntok > 0 ? (int)(((int64_t)ntok * group + kXBM - 1) / kXBM) : 0;
+// Row tiles of bm rows of a sequence with ntok query tokens.
+__device__ __forceinline__ int seq_row_tiles(int ntok, int group, int bm) {
+  return ntok > 0 ? (int)(((int64_t)ntok * group + bm - 1) / bm) : 0;
 }
 
 // Block-wide exclusive prefix sum of one value per thread (kPlanThreads threads);
@@ -157,7 +165,7 @@ __global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const Exte
   int carry = 0;
   for (int base = 0; base < a.batch; base += kPlanThreads) {
     const int b = base + tid;
-    const int n = b < a.batch ? seq_row_tiles(qsl[b + 1] - qsl[b], a.group) : 0;
+    const int n = b < a.batch ? seq_row_tiles(qsl[b + 1] - qsl[b], a.group, a.tile_rows) : 0;
     int total;
     const int off = block_exclusive_scan(n, sums, &total);
     if (b < a.batch) start[b] = carry + off;
@@ -180,10 +188,10 @@ __global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const Exte
     const int ntok = qsl[b + 1] - qsl[b];
     const int seq = seq_lens[b];
     const int prefix = a.prefix ? gptr(a.prefix)[b] : seq - ntok;
-    const KeyRange k = row_tile_keys(rt * kXBM, ntok, a.group, prefix, seq, a.causal, a.window);
+    const KeyRange k = row_tile_keys(rt * a.tile_rows, a.tile_rows, ntok, a.group, prefix, seq, a.causal, a.window);
     *b_out = b;
     *rt_out = rt;
-    return (k.hi > k.lo ? (k.hi - k.lo + kXBN - 1) / kXBN : 0) + kPlanFixedCost;
+    return (k.hi > k.lo ? (k.hi - k.lo + a.tile_keys - 1) / a.tile_keys : 0) + kPlanFixedCost;
   };
 
   // 2. the largest cost, which scales the classes
@@ -224,14 +232,42 @@ __global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const Exte
   for (int i = m + tid; i < a.capacity; i += kPlanThreads) items[i] = row_tile_item(-1, -1);
 }
 
-template <bool QBF16, int KV>
+// maximum of N values by three-input maxima (which also skip the quieting v_max that
+// the compiler puts on MFMA results)
+template <int N>
+__device__ __forceinline__ float max_tree(const float* v) {
+  if constexpr (N == 1) {
+    return v[0];
+  } else if constexpr (N == 2) {
+    return max3f(v[0], v[1], -INFINITY);
+  } else {
+    constexpr int M = (N + 2) / 3;
+    float w[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+      w[i] = 3 * i + 2 < N ? max3f(v[3 * i], v[3 * i + 1], v[3 * i + 2])
+                           : (3 * i + 1 < N ? max3f(v[3 * i], v[3 * i + 1], -INFINITY) : v[3 * i]);
+    return max_tree<M>(w);
+  }
+}
+
+template <int D, bool QBF16, int KV>
 __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArgs args) {
   const ExtendArgs a = args;  // local copy: the lambdas capture by reference
+  constexpr int kXD = D;
+  constexpr int kXBN = XShape<D>::BN;
+  constexpr int kXRB = XShape<D>::RB;
+  constexpr int kXBM = XShape<D>::BM;
+  constexpr int KK = D / 32;                     // QK MFMA steps (16-bit operands)
+  constexpr int KB = kXBN / 16;                  // 16-key blocks per tile
+  constexpr int DB = D / 16;                     // PV MFMA steps
+  constexpr int HF = kXBN / 32;                  // 32-key halves of a tile (PV contraction)
   constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
   constexpr bool kConvV = (!kFp8) && QBF16;      // bf16 V: converted to fp16 in LDS
   constexpr int kElt = kFp8 ? 1 : 2;
-  constexpr int kKSub = kFp8 ? 2 : 4;            // K DMA blocks per 16-key block
   constexpr int kRowB = kXD * kElt;              // bytes of one K/V row
+  constexpr int kKSub = kRowB / 64;              // K DMA blocks (1 KB) per 16-key block
+  constexpr int kCPR = kRowB / 16;               // 16-byte chunks per row
   constexpr int kStageB = kXBN * kRowB;          // bytes of the K (or V) part of a tile
   constexpr int kKBlk = kStageB / 1024 / kXWaves;  // K DMA blocks per wave per tile
   constexpr int kVBlk = kStageB / 1024 / kXWaves;  // V DMA blocks per wave per tile
@@ -245,6 +281,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   // step k-2 (tile k is issued at step k-S+1 <= k-3)
   static_assert(S >= 4, "the schedule needs at least four stages");
   static_assert(kKBlk >= 1 && kKSub % kKBlk == 0, "a wave's K blocks share one key block");
+  static_assert(kVBlk >= 1 && 64 % kCPR == 0, "a V DMA block holds whole rows");
 
   __shared__ __attribute__((aligned(1024))) unsigned char kring[S][kStageB];
   __shared__ __attribute__((aligned(1024))) unsigned char vring[S][kStageB];
@@ -271,7 +308,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   // ---- this lane's rows (one per 16-row block) ----
   int lo_r[kXRB], hi_r[kXRB];
   bool real[kXRB];
-  u32x4 qv[kXRB][4];
+  u32x4 qv[kXRB][KK];
   const uint16_t MA_GLOBAL* qbase = gptr(reinterpret_cast<const uint16_t*>(a.q));
 #pragma unroll
   for (int rb = 0; rb < kXRB; ++rb) {
@@ -283,15 +320,15 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     lo_r[rb] = (real[rb] && a.window >= 0) ? max(0, qpos - a.window) : 0;
     hi_r[rb] = real[rb] ? (a.causal ? min(seq, qpos + 1) : seq) : 0;
     const uint16_t MA_GLOBAL* qp =
-        qbase + (int64_t)(tok0 + t) * a.q_stride_tok + (int64_t)(h * a.group + g) * a.q_stride_head + j * 32;
+        qbase + (int64_t)(tok0 + t) * a.q_stride_tok + (int64_t)(h * a.group + g) * a.q_stride_head + j * (kXD / 4);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int kk = 0; kk < KK; ++kk)
       qv[rb][kk] = real[rb] ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + kk * 8) : u32x4{0, 0, 0, 0};
   }
   // keys any row of the workgroup may see, and the window in which no row needs masking
   const int t_first = r0 / a.group;
   const int t_last = min(ntok - 1, (r0 + kXBM - 1) / a.group);
-  const KeyRange keys = row_tile_keys(r0, ntok, a.group, prefix, seq, a.causal, a.window);
+  const KeyRange keys = row_tile_keys(r0, kXBM, ntok, a.group, prefix, seq, a.causal, a.window);
   const int key_lo = keys.lo;
   const int key_hi = keys.hi;
   const int full_lo = a.window >= 0 ? max(0, prefix + t_last - a.window) : 0;
@@ -299,7 +336,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   const int ntiles = key_hi > key_lo ? (key_hi - key_lo + kXBN - 1) / kXBN : 0;
 
   float m_run[kXRB];
-  f32x4 o[kXRB][8];
+  f32x4 o[kXRB][DB];
   // row sums of P, by MFMA: A = a 16 x 32 block whose row 0 is ones, so D[0][row] = sum_k P[row][k]
   f32x4 lacc[kXRB];
   const uint32_t one2 = (c == 0) ? 0x3C003C00u : 0u;
@@ -309,7 +346,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     m_run[rb] = -INFINITY;
     lacc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int db = 0; db < 8; ++db) o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < DB; ++db) o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   const unsigned char MA_GLOBAL* kbase = gptr(reinterpret_cast<const unsigned char*>(a.k));
@@ -317,7 +354,12 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   const int64_t row_bytes = a.kv_stride_row * kElt;
   const uint32_t row_bytes32 = (uint32_t)row_bytes;  // the host checks it fits
   const int64_t head_off = (int64_t)h * a.kv_stride_head * kElt;
-  auto swz = [](int t) -> int { return kFp8 ? ((t & 3) | ((t >> 2) & 4)) : ((2 * t) & 15); };
+  // XOR swizzle of the 16-byte chunks of V row t in LDS (spreads the transposed reads
+  // over the banks); it stays below the row's chunk count
+  auto swz = [](int t) -> int {
+    if constexpr (kFp8) return kCPR >= 8 ? ((t & 3) | ((t >> 2) & 4)) : (t & (kCPR - 1));
+    else return (2 * t) & (kCPR - 2);
+  };
 
   // ---- memory pipeline ----
   // Lane l looks up the slot of key l of a tile; tiles past the last are clamped to it
@@ -351,7 +393,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
 #pragma unroll
     for (int x = 0; x < kVBlk; ++x) {
       const int xb = wave * kVBlk + x;
-      vslot[x] = shfl_i(myslot, kFp8 ? (8 * xb + (lane >> 3)) : (4 * xb + (lane >> 4)));
+      vslot[x] = shfl_i(myslot, (64 / kCPR) * xb + lane / kCPR);
     }
     // K: lane l -> key kb_w*16 + (l & 15), 16-byte chunk kKSub*j + sub
     const unsigned char MA_GLOBAL* kp = kbase + (uint64_t)(uint32_t)kslot * row_bytes32 + head_off;
@@ -364,8 +406,8 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
 #pragma unroll
     for (int x = 0; x < kVBlk; ++x) {
       const int xb = wave * kVBlk + x;
-      const int tok = kFp8 ? (8 * xb + (lane >> 3)) : (4 * xb + (lane >> 4));
-      const int pos = kFp8 ? (lane & 7) : (lane & 15);
+      const int tok = (64 / kCPR) * xb + lane / kCPR;
+      const int pos = lane % kCPR;
       dma(vbase + (uint64_t)(uint32_t)vslot[x] * row_bytes32 + head_off + ((pos ^ swz(tok)) << 4), vl + xb * 1024);
     }
   };
@@ -388,7 +430,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   };
   // per-lane part of the V^T read addresses (16-bit V): row 4j + e, column bits of cc
   const int vrow = (4 * j + (c >> 2)) * kRowB + ((lane & 3) >> 1) * 16 + (lane & 1) * 8;
-  const int vs1 = (4 * j + (c >> 2)) & 7;
+  const int vs1 = (4 * j + (c >> 2)) & (kCPR / 2 - 1);
 
   // ---- one tile: scores for all 64 keys, then mid() (work that overlaps the score
   // MFMAs), one softmax update, PV ----
@@ -396,17 +438,17 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     const unsigned char* kt = kring[st];
     const unsigned char* vt = vring[st];
     const int base = key_lo + tile * kXBN;
-    f32x4 s[kXRB][4];
+    f32x4 s[kXRB][KB];
 #pragma unroll
     for (int rb = 0; rb < kXRB; ++rb)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) s[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < KB; ++kb) s[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (kFp8) {
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
+      for (int hh = 0; hh < kKSub; ++hh)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const u32x4 raw = *reinterpret_cast<const u32x4*>(kt + (kb * 2 + hh) * 1024 + lane * 16);
+        for (int kb = 0; kb < KB; ++kb) {
+          const u32x4 raw = *reinterpret_cast<const u32x4*>(kt + (kb * kKSub + hh) * 1024 + lane * 16);
           u32x4 k0, k1;
           cvt16_fp8<KV, QBF16>(raw, k0, k1);
 #pragma unroll
@@ -417,37 +459,36 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
         }
     } else {
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
+      for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(kt + (kb * 4 + kk) * 1024 + lane * 16);
+        for (int kb = 0; kb < KB; ++kb) {
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(kt + (kb * kKSub + kk) * 1024 + lane * 16);
 #pragma unroll
           for (int rb = 0; rb < kXRB; ++rb) s[rb][kb] = mfma16t<QBF16>(kf, qv[rb][kk], s[rb][kb]);
         }
     }
     mid();
     const bool full = (base >= full_lo) && (base + kXBN <= full_hi);
-    u32x4 pk[kXRB][2];
+    u32x4 pk[kXRB][HF];
     float alpha[kXRB];
     bool grew = false;
 #pragma unroll
     for (int rb = 0; rb < kXRB; ++rb) {
       if (!full) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int pos = base + kb * 16 + 4 * j + i;
             if (pos < lo_r[rb] || pos >= hi_r[rb]) s[rb][kb][i] = -INFINITY;
           }
       }
-      const f32x4* sr = s[rb];
-      const float m0 = max3f(sr[0][0], sr[0][1], sr[0][2]);
-      const float m1 = max3f(sr[0][3], sr[1][0], sr[1][1]);
-      const float m2 = max3f(sr[1][2], sr[1][3], sr[2][0]);
-      const float m3 = max3f(sr[2][1], sr[2][2], sr[2][3]);
-      const float m4 = max3f(sr[3][0], sr[3][1], sr[3][2]);
-      float mx = max3f(max3f(m0, m1, m2), max3f(m3, m4, sr[3][3]), -INFINITY);
+      float sv[4 * KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[kb * 4 + i] = s[rb][kb][i];
+      float mx = max_tree<4 * KB>(sv);
       alpha[rb] = 1.f;
       // the exponent base only moves when some row's max has grown by more than
       // 2^kLazyRescale in p: until then p stays <= 2^kLazyRescale (exact in fp16's
@@ -463,14 +504,14 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       }
       const float m_use = (m_run[rb] == -INFINITY) ? 0.f : m_run[rb];
       const float msc = m_use * a.scale_log2;
-      float p[16];
+      float p[4 * KB];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[kb * 4 + i] = __builtin_amdgcn_exp2f(s[rb][kb][i] * a.scale_log2 - msc);
 
 #pragma unroll
-      for (int st2 = 0; st2 < 2; ++st2)
+      for (int st2 = 0; st2 < HF; ++st2)
 #pragma unroll
         for (int w = 0; w < 4; ++w) pk[rb][st2][w] = pack_f16(p[8 * st2 + 2 * w], p[8 * st2 + 2 * w + 1]);
     }
@@ -478,14 +519,14 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
 #pragma unroll
       for (int rb = 0; rb < kXRB; ++rb)
 #pragma unroll
-        for (int db = 0; db < 8; ++db) o[rb][db] *= alpha[rb];
+        for (int db = 0; db < DB; ++db) o[rb][db] *= alpha[rb];
 #pragma unroll
       for (int rb = 0; rb < kXRB; ++rb) lacc[rb] *= alpha[rb];
     }
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
+    for (int hf = 0; hf < HF; ++hf)
 #pragma unroll
-      for (int db = 0; db < 8; ++db) {
+      for (int db = 0; db < DB; ++db) {
         u32x4 va;
         if constexpr (kFp8) {
           const int e = c >> 1, cc = lane & 1;
@@ -509,7 +550,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
         for (int rb = 0; rb < kXRB; ++rb) o[rb][db] = mfma16t<false>(va, pk[rb][hf], o[rb][db]);
       }
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
+    for (int hf = 0; hf < HF; ++hf)
 #pragma unroll
       for (int rb = 0; rb < kXRB; ++rb) lacc[rb] = mfma16t<false>(ones, pk[rb][hf], lacc[rb]);
   };
@@ -583,7 +624,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) + (int64_t)(tok0 + t) * a.out_stride_tok +
                              (int64_t)(h * a.group + g) * a.out_stride_head;
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
+    for (int db = 0; db < DB; ++db) {
       u32x2 w;
       w[0] = (uint32_t)f2h<QBF16>(o[rb][db][0] * inv) | ((uint32_t)f2h<QBF16>(o[rb][db][1] * inv) << 16);
       w[1] = (uint32_t)f2h<QBF16>(o[rb][db][2] * inv) | ((uint32_t)f2h<QBF16>(o[rb][db][3] * inv) << 16);
@@ -592,28 +633,45 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   }
 }
 
-template <bool QBF16>
+template <int D, bool QBF16>
 static hipError_t launch_extend_q(int kv, dim3 grid, hipStream_t st, const ExtendArgs& a) {
-  switch (kv) {
-    case DT_E4M3: hipLaunchKernelGGL((extend_kernel<QBF16, DT_E4M3>), grid, dim3(kXWaves * 64), 0, st, a); break;
-    case DT_E5M2: hipLaunchKernelGGL((extend_kernel<QBF16, DT_E5M2>), grid, dim3(kXWaves * 64), 0, st, a); break;
-    default: hipLaunchKernelGGL((extend_kernel<QBF16, QBF16 ? DT_BF16 : DT_F16>), grid, dim3(kXWaves * 64), 0, st, a);
+  if constexpr (D > 64) {  // at D = 64 an fp8 tile is too small for one 1 KB block per wave
+    if (kv == DT_E4M3) {
+      hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E4M3>), grid, dim3(kXWaves * 64), 0, st, a);
+      return hipGetLastError();
+    }
+    if (kv == DT_E5M2) {
+      hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E5M2>), grid, dim3(kXWaves * 64), 0, st, a);
+      return hipGetLastError();
+    }
   }
+  hipLaunchKernelGGL((extend_kernel<D, QBF16, QBF16 ? DT_BF16 : DT_F16>), grid, dim3(kXWaves * 64), 0, st, a);
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_extend_d(bool qbf16, int kv, dim3 grid, hipStream_t st, const ExtendArgs& a) {
+  return qbf16 ? launch_extend_q<D, true>(kv, grid, st, a) : launch_extend_q<D, false>(kv, grid, st, a);
 }
 
 }  // namespace ma
 
 using namespace ma;
 
-static int64_t extend_items(int64_t num_tokens, int group, int batch) {
-  // sum over sequences of ceil(ntok * G / kXBM) <= num_tokens * G / kXBM + batch
-  return (num_tokens * group + kXBM - 1) / kXBM + batch;
+static int64_t extend_items(int64_t num_tokens, int group, int batch, int bm) {
+  // sum over sequences of ceil(ntok * G / bm) <= num_tokens * G / bm + batch
+  return (num_tokens * group + bm - 1) / bm + batch;
+}
+
+// Rows per workgroup of the extend kernel at a head dim (0 if unsupported).
+static int extend_tile_rows(int head_dim) {
+  return head_dim == 64 ? XShape<64>::BM : head_dim == 128 ? XShape<128>::BM : head_dim == 256 ? XShape<256>::BM : 0;
 }
 
 extern "C" size_t ma_extend_workspace_bytes(int64_t num_tokens, int num_q_heads, int num_kv_heads, int batch) {
   if (num_tokens < 0 || batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return 0;
-  const int64_t n = extend_items(num_tokens, num_q_heads / num_kv_heads, batch);
+  // sized for the smallest row tile, so one workspace serves every head dim
+  const int64_t n = extend_items(num_tokens, num_q_heads / num_kv_heads, batch, kXBMMin);
   return ((size_t)n * sizeof(int64_t) + 255) & ~(size_t)255;
 }
 
@@ -626,7 +684,10 @@ extern "C" int ma_paged_extend(
     int causal, int sliding_window, float softmax_scale, float k_scale, float v_scale,
     void* workspace, size_t workspace_bytes, void* out, int64_t out_stride_tok, int64_t out_stride_head,
     void* stream) {
-  if (head_dim != kXD) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (128)", head_dim);
+  const int bm = extend_tile_rows(head_dim);
+  if (bm == 0) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (64, 128 or 256)", head_dim);
+  if (head_dim == 64 && (kv_dtype == DT_E4M3 || kv_dtype == DT_E5M2))
+    return set_error(MA_EUNSUPPORTED, "fp8 KV at head_dim 64 is not supported");
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
   if (kv_dtype < 0 || kv_dtype > DT_E5M2) return set_error(MA_EINVAL, "kv dtype %d unknown", kv_dtype);
   if ((kv_dtype == DT_F16 || kv_dtype == DT_BF16) && kv_dtype != q_dtype)
@@ -650,7 +711,7 @@ extern "C" int ma_paged_extend(
       ((q_stride_head * 2) & 15) || ((out_stride_tok * 2) & 7) || ((out_stride_head * 2) & 7))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   const int group = num_q_heads / num_kv_heads;
-  const int64_t items = extend_items(num_tokens, group, batch);
+  const int64_t items = extend_items(num_tokens, group, batch, bm);
   if (items * num_kv_heads > 0x7fffffff / (kXWaves * 64)) return set_error(MA_EINVAL, "grid too large");
   const size_t need = ma_extend_workspace_bytes(num_tokens, num_q_heads, num_kv_heads, batch);
   if (!workspace || workspace_bytes < need)
@@ -659,6 +720,7 @@ extern "C" int ma_paged_extend(
   ExtendPlanArgs p{};
   p.qsl = query_start_loc; p.seq_lens = seq_lens; p.prefix = prefix_lens;
   p.batch = batch; p.group = group; p.causal = causal ? 1 : 0; p.window = sliding_window < 0 ? -1 : sliding_window;
+  p.tile_rows = bm; p.tile_keys = head_dim == 256 ? XShape<256>::BN : XShape<128>::BN;
   p.capacity = (int)items; p.items = reinterpret_cast<int64_t*>(workspace);
   hipLaunchKernelGGL(extend_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
@@ -674,8 +736,10 @@ extern "C" int ma_paged_extend(
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
   const dim3 grid((unsigned)(items * num_kv_heads));
-  e = (q_dtype == DT_BF16) ? launch_extend_q<true>(kv_dtype, grid, (hipStream_t)stream, a)
-                           : launch_extend_q<false>(kv_dtype, grid, (hipStream_t)stream, a);
+  const bool qbf16 = q_dtype == DT_BF16;
+  e = head_dim == 64    ? launch_extend_d<64>(qbf16, kv_dtype, grid, (hipStream_t)stream, a)
+      : head_dim == 128 ? launch_extend_d<128>(qbf16, kv_dtype, grid, (hipStream_t)stream, a)
+                        : launch_extend_d<256>(qbf16, kv_dtype, grid, (hipStream_t)stream, a);
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "extend launch failed: %s", hipGetErrorString(e));
   return MA_OK;
 }

@@ -35,9 +35,11 @@
 //                                     back transposed (ds_read_b64_tr_b16 / _tr_b8).
 //   bf16 V: P split into two bf16 halves (exact to ~16 bits); fp16 / fp8 V: fp16 P.
 //
+// Head dims 64, 128 and 256; the configuration measured and tuned is D = 128.
+//
 // Memory pipeline: K and V of the next S-1 tiles are in flight while a tile computes
-// (S = 4 for 16-bit KV, 8 for fp8: about 100-200 KB per CU; random 256-byte row gathers
-// need that much in flight to approach HBM bandwidth). K rows land in an AGPR ring in
+// (at D = 128, S = 4 for 16-bit KV and 8 for fp8: about 100-200 KB per CU; random
+// 256-byte row gathers need that much in flight to approach HBM bandwidth). K rows land in an AGPR ring in
 // MFMA operand layout; V rows go straight to a per-wave LDS ring by DMA
 // (global_load_lds). Slots are looked up 2S-3 tiles ahead of compute. All of these are
 // issued as inline assembly and waited for with explicit counts. The issue cursor clamps
@@ -268,14 +270,8 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   // A local copy: the lambdas below capture by reference, and a reference to the kernel
   // argument itself would force it into scratch memory.
   const SplitKVArgs a = args;
-  static_assert(D == 128, "head dim 128");
+  static_assert(D == 64 || D == 128 || D == 256, "head dim 64, 128 or 256");
   constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
-  // pipeline stages: K of S tiles in a register ring, V of S tiles in an LDS ring
-  // (S * 8 KB per wave for 16-bit KV, S * 4 KB for fp8). Each step issues OPS vector
-  // memory instructions (one slot lookup, the V DMA, the K loads); a wave can have at
-  // most 63 outstanding, which bounds S.
-  constexpr int S = kFp8 ? 8 : 4;
-  constexpr int A = 2 * S - 3;  // slots are looked up A tiles ahead of compute
   constexpr int KK = D / 32;          // QK MFMA steps
   constexpr int DB = D / 16;          // PV MFMA steps
   constexpr int DQ = D / 4;           // head-dim entries per lane group in QK
@@ -284,11 +280,21 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   constexpr bool kSplitP = kPvBf16;
   constexpr int kElt = kFp8 ? 1 : 2;
   constexpr int kRowB = D * kElt;           // bytes of one head row
+  constexpr int kCPR = kRowB / 16;          // 16-byte chunks per row
   constexpr int kStage = kTile * kRowB;     // bytes of one V tile
   constexpr int kVL = kStage / 1024;        // 16-byte V loads per lane per tile
   constexpr int KR = kFp8 ? KK / 2 : KK;    // 16-byte K loads per lane per 16-token block
   constexpr int OPS = 1 + kVL + 2 * KR;     // vector memory instructions per pipeline step
-  static_assert((S - 1) * OPS <= 63, "more outstanding loads than the counter holds");
+  // Pipeline stages: K of S tiles in a register ring, V of S tiles in an LDS ring. Each
+  // step issues OPS vector memory instructions (one slot lookup, the V DMA, the K loads);
+  // a wave can have at most 63 outstanding, which bounds S: 4 for 16-bit KV at D=128
+  // (more stages measured no faster), 8 where the counter allows it (fp8, D=64), and 2
+  // for 16-bit KV at D=256, whose 32-token tile takes 33 instructions.
+  constexpr int kSMax = 63 / OPS + 1;
+  constexpr int S = (kFp8 || D == 64) ? (kSMax < 8 ? kSMax : 8) : (kSMax < 4 ? kSMax : 4);
+  constexpr int A = 2 * S - 3;  // slots are looked up A tiles ahead of compute
+  static_assert(S >= 2 && (S - 1) * OPS <= 63, "more outstanding loads than the counter holds");
+  static_assert(kVL >= 1 && 64 % kCPR == 0, "a V load covers whole rows");
 
   __shared__ __attribute__((aligned(16))) unsigned char vring[kWaves][S][kStage];
 
@@ -322,7 +328,12 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   const int64_t row_bytes = a.kv_stride_row * kElt;
   const int64_t head_bytes = a.kv_stride_head * kElt;
 
-  auto swz = [](int t) -> int { return kFp8 ? ((t & 3) | ((t >> 2) & 4)) : ((2 * t) & 15); };
+  // XOR swizzle of the 16-byte chunks of V row t in LDS (spreads the transposed reads
+  // over the banks); it stays below the row's chunk count
+  auto swz = [](int t) -> int {
+    if constexpr (kFp8) return kCPR >= 8 ? ((t & 3) | ((t >> 2) & 4)) : (t & (kCPR - 1));
+    else return (2 * t) & (kCPR - 2);
+  };
 
   // ---- per-tile K register ring (V goes to the LDS ring by DMA) ----
   struct Raw {
@@ -362,8 +373,9 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)vring[wave][stage];
 #pragma unroll
     for (int x = 0; x < kVL; ++x) {
-      const int tok = kFp8 ? (8 * x + (lane >> 3)) : (4 * x + (lane >> 4));
-      const int pos = kFp8 ? (lane & 7) : (lane & 15);
+      // one instruction: 64 / kCPR whole rows, lane -> (row, 16-byte chunk)
+      const int tok = (64 / kCPR) * x + lane / kCPR;
+      const int pos = lane % kCPR;
       const int slot = shfl_i(myslot, tok);
       const unsigned char MA_GLOBAL* src = vbase + (int64_t)slot * row_bytes + hoff + ((pos ^ swz(tok)) << 4);
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + x * 1024);
@@ -679,8 +691,9 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       // flight through the compute: no DMA then writes the LDS ring while the tile's
       // transposed V reads run. fp8 KV, half the bytes per tile: only tile n, so S-1
       // tiles stay in flight, which is 12% faster than waiting for all (3 to 7 tiles
-      // in flight measured the same).
-      wait_vm(std::integral_constant<int, kFp8 ? (S - 1) * OPS : 0>{});
+      // in flight measured the same). With S = 2 (16-bit KV at D=256) the wait for the
+      // slot above has already drained tile n, and tile n+1 stays in flight.
+      wait_vm(std::integral_constant<int, (kFp8 || S < 4) ? (S - 1) * OPS : 0>{});
       touch_k(ring[I]);
       compute(cc, ring[I], I);
       const bool seg_last = (cc.tile == cc.g.nt - 1);
@@ -722,7 +735,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
 // segment, combine the pieces of waves w1..W into the output: a running maximum of the
 // log2 LSEs rescales the sum of the normalised partial outputs, so one pass reads each
 // piece once and the loads of successive pieces do not wait for each other's math.
-// 256 threads cover 8 rows x 128 head-dim entries per pass.
+// 256 threads cover 1024 / D rows x D head-dim entries per pass.
 // ---------------------------------------------------------------------------
 template <int D, int NB, bool QBF16>
 __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
@@ -735,20 +748,26 @@ __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
   const Geom g = geom_u(a, b);
   const float MA_GLOBAL* plse = gptr(a.part_lse);
   const float MA_GLOBAL* po = gptr(a.part_o);
-  const int d4 = (threadIdx.x & 31) * 4;
-  // thread: rows (threadIdx.x >> 5) + 8 i, head-dim entries d4..d4+3, taken kChunk row
-  // sets at a time; within a chunk the pieces are the outer loop (unrolled by four), so
-  // the loads of a chunk's rows and of four pieces are in flight together. Measured: one
-  // chunk of all four row sets for 32-row groups (13 -> 10 us on a verify batch of 32 x 4
-  // tokens), one row set per chunk for 16-row groups, whose second set is padding when
-  // G = 8 (about 5 us on a decode batch of 64).
-  constexpr int kPass = kRows / 8;
+  constexpr int kTPR = D / 4;       // threads per row, four head-dim entries each
+  constexpr int kRPP = 256 / kTPR;  // rows per pass of the workgroup
+  const int d4 = (threadIdx.x % kTPR) * 4;
+  const int r_base = threadIdx.x / kTPR;
+  // thread: rows r_base + kRPP i, head-dim entries d4..d4+3, taken kChunk row sets at a
+  // time; within a chunk the pieces are the outer loop (unrolled by four), so the loads
+  // of a chunk's rows and of four pieces are in flight together. Measured at D=128: one
+  // chunk of all four row sets for 32-row groups (13 -> 10 us on a verify batch of
+  // 32 x 4 tokens), one row set per chunk for 16-row groups, whose second set is padding
+  // when G = 8 (about 5 us on a decode batch of 64).
+  constexpr int kPass = kRows / kRPP > 0 ? kRows / kRPP : 1;
   constexpr int kChunk = (NB == 1) ? 1 : kPass;
 #pragma unroll
   for (int c0 = 0; c0 < kPass; c0 += kChunk) {
     bool live = false;  // rows past the last query token (GQA padding) are not read
 #pragma unroll
-    for (int i = 0; i < kChunk; ++i) live |= (rg * kRows + (threadIdx.x >> 5) + 8 * (c0 + i)) / a.group < g.ntok;
+    for (int i = 0; i < kChunk; ++i) {
+      const int row = r_base + kRPP * (c0 + i);
+      live |= row < kRows && (rg * kRows + row) / a.group < g.ntok;
+    }
     if (!live) continue;
     float m[kChunk], wsum[kChunk];
     f32x4 acc[kChunk];
@@ -760,13 +779,13 @@ __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
     }
 #pragma unroll 4
     for (int w = w1; w <= W; ++w) {
-      const int64_t pbase = ((int64_t)w * 2 + (w == w1 ? sel1 : 0)) * kMaxRows + (threadIdx.x >> 5) + 8 * c0;
+      const int64_t pbase = ((int64_t)w * 2 + (w == w1 ? sel1 : 0)) * kMaxRows + r_base + kRPP * c0;
       float lse[kChunk];
       f32x4 o[kChunk];
 #pragma unroll
       for (int i = 0; i < kChunk; ++i) {
-        lse[i] = plse[pbase + 8 * i];
-        o[i] = *reinterpret_cast<const f32x4 MA_GLOBAL*>(po + (pbase + 8 * i) * D + d4);
+        lse[i] = plse[pbase + kRPP * i];
+        o[i] = *reinterpret_cast<const f32x4 MA_GLOBAL*>(po + (pbase + kRPP * i) * D + d4);
       }
 #pragma unroll
       for (int i = 0; i < kChunk; ++i) {
@@ -780,11 +799,11 @@ __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
     }
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
-      const int row = (threadIdx.x >> 5) + 8 * (c0 + i);
+      const int row = r_base + kRPP * (c0 + i);
       const int R = rg * kRows + row;
       const int t = R / a.group;
       const int gg = R - t * a.group;
-      if (t >= g.ntok) continue;
+      if (row >= kRows || t >= g.ntok) continue;
       uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) +
                                (int64_t)(g.tok0 + t) * a.out_stride_tok +
                                (int64_t)(h * a.group + gg) * a.out_stride_head + d4;
@@ -803,10 +822,32 @@ static hipError_t launch_partial_kv(int kv, dim3 grid, hipStream_t st, const Spl
   return hipGetLastError();
 }
 
+// Row blocks per row group: at D = 256 only one (two would spill registers that in-flight
+// loads still target); the host then uses more row groups of 16 rows.
+template <int D>
+constexpr int kMaxNB = D == 256 ? 1 : 2;
+
 template <int D>
 static hipError_t launch_partial_d(int nb, bool qbf16, int kv, dim3 grid, hipStream_t st, const SplitKVArgs& a) {
-  if (qbf16) return nb == 1 ? launch_partial_kv<D, 1, true>(kv, grid, st, a) : launch_partial_kv<D, 2, true>(kv, grid, st, a);
-  return nb == 1 ? launch_partial_kv<D, 1, false>(kv, grid, st, a) : launch_partial_kv<D, 2, false>(kv, grid, st, a);
+  if constexpr (kMaxNB<D> == 1) {
+    return qbf16 ? launch_partial_kv<D, 1, true>(kv, grid, st, a) : launch_partial_kv<D, 1, false>(kv, grid, st, a);
+  } else {
+    if (qbf16) return nb == 1 ? launch_partial_kv<D, 1, true>(kv, grid, st, a) : launch_partial_kv<D, 2, true>(kv, grid, st, a);
+    return nb == 1 ? launch_partial_kv<D, 1, false>(kv, grid, st, a) : launch_partial_kv<D, 2, false>(kv, grid, st, a);
+  }
+}
+
+template <int D>
+static hipError_t launch_merge_d(int nb, bool qbf16, dim3 grid, hipStream_t st, const SplitKVArgs& a) {
+  constexpr int NB2 = kMaxNB<D>;
+  if (qbf16) {
+    if (nb == 1) hipLaunchKernelGGL((splitkv_merge<D, 1, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((splitkv_merge<D, NB2, true>), grid, dim3(256), 0, st, a);
+  } else {
+    if (nb == 1) hipLaunchKernelGGL((splitkv_merge<D, 1, false>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((splitkv_merge<D, NB2, false>), grid, dim3(256), 0, st, a);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace ma
@@ -844,7 +885,8 @@ extern "C" int ma_device_workgroups(void) { return device_workgroups(0); }
 
 static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, int max_q_per_seq,
                        int num_workgroups, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (head_dim != 128) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (128)", head_dim);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (64, 128 or 256)", head_dim);
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
   if (kv_dtype < 0 || kv_dtype > DT_E5M2) return set_error(MA_EINVAL, "kv dtype %d unknown", kv_dtype);
   if ((kv_dtype == DT_F16 || kv_dtype == DT_BF16) && kv_dtype != q_dtype)
@@ -868,7 +910,7 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   a.group = a.hq / a.hkv;
   const int rows_total = max_q_per_seq * a.group;
-  const int nb = rows_total <= 16 ? 1 : 2;
+  const int nb = (rows_total <= 16 || head_dim == 256) ? 1 : 2;
   a.rows = 16 * nb;
   a.row_groups = (rows_total + a.rows - 1) / a.rows;
   a.nwaves = num_workgroups * kWaves;
@@ -882,17 +924,16 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
   a.part_lse = reinterpret_cast<float*>(ws + ws_desc_bytes(num_workgroups) + ws_o_bytes(num_workgroups, head_dim));
   const int64_t segs = (int64_t)a.batch * a.hkv * a.row_groups;
   if (segs > 0x7fffffff) return set_error(MA_EINVAL, "too many segments");
-  hipError_t e = launch_partial_d<128>(nb, q_dtype == DT_BF16, kv_dtype, dim3(num_workgroups), stream, a);
+  const bool qbf16 = q_dtype == DT_BF16;
+  const dim3 grid((unsigned)num_workgroups);
+  hipError_t e = head_dim == 64    ? launch_partial_d<64>(nb, qbf16, kv_dtype, grid, stream, a)
+                 : head_dim == 128 ? launch_partial_d<128>(nb, qbf16, kv_dtype, grid, stream, a)
+                                   : launch_partial_d<256>(nb, qbf16, kv_dtype, grid, stream, a);
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "split-KV launch failed: %s", hipGetErrorString(e));
   const dim3 mgrid((unsigned)a.nwaves);  // one workgroup per partial-kernel wave
-  if (q_dtype == DT_BF16) {
-    if (nb == 1) hipLaunchKernelGGL((splitkv_merge<128, 1, true>), mgrid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((splitkv_merge<128, 2, true>), mgrid, dim3(256), 0, stream, a);
-  } else {
-    if (nb == 1) hipLaunchKernelGGL((splitkv_merge<128, 1, false>), mgrid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((splitkv_merge<128, 2, false>), mgrid, dim3(256), 0, stream, a);
-  }
-  e = hipGetLastError();
+  e = head_dim == 64    ? launch_merge_d<64>(nb, qbf16, mgrid, stream, a)
+      : head_dim == 128 ? launch_merge_d<128>(nb, qbf16, mgrid, stream, a)
+                        : launch_merge_d<256>(nb, qbf16, mgrid, stream, a);
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "merge launch failed: %s", hipGetErrorString(e));
   return MA_OK;
 }

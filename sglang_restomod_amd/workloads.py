@@ -1,7 +1,8 @@
-"""Seeded generators for the five benchmark workloads.
+"""Seeded generators for the benchmark workloads: five at head dim 128 (0-4) and two
+at head dim 256 (5, 6).
 
 Seeding scheme: one CPU ``torch.Generator`` per workload with seed = workload
-index 0..4. Draw order: lengths, slot permutation, then (on the target device,
+index. Draw order: lengths, slot permutation, then (on the target device,
 with a device generator of the same seed) q, k, v, then scales, then the request
 row permutation. The pool has ``sum(seq_len) + 1`` slots; slot 0 is padding, as
 in SGLang's token pool. Slots are one global ``randperm`` split across requests,
@@ -30,6 +31,12 @@ WORKLOADS = {
             heads=32, heads_kv=8, dim=128, dtype="bf16", kv="fp8"),
     4: dict(name="verify_b32_t4_p2k-16k_h64kv8_d128_bf16", mode="verify", batch=32, prefix=(2048, 16384),
             draft=4, heads=64, heads_kv=8, dim=128, dtype="bf16", kv="bf16"),
+    # head dim 256 at a 27B model's two-GPU share (12 query heads, 2 kv heads), the shape
+    # of the reference's own D256 kernels
+    5: dict(name="decode_b64_ctx1k-8k_h12kv2_d256_bf16", mode="decode", batch=64, ctx=(1024, 8192),
+            heads=12, heads_kv=2, dim=256, dtype="bf16", kv="bf16"),
+    6: dict(name="extend_b8_p0-4k_e256-2k_h12kv2_d256_bf16", mode="extend", batch=8,
+            prefix=(0, 4096), extend=(256, 2048), heads=12, heads_kv=2, dim=256, dtype="bf16", kv="bf16"),
 }
 
 _DT = {"fp16": torch.float16, "bf16": torch.bfloat16}

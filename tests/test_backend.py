@@ -33,8 +33,20 @@ def test_registry_factory_builds_the_backend():
 
 
 def test_unsupported_head_dim_is_refused_at_construction():
-    eng = _engine(head_dim=64)
+    eng = _engine(head_dim=96)
     with pytest.raises(NotImplementedError, match="head_dim"):
+        _backend(eng)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_supported_head_dims_construct(head_dim):
+    be = _backend(_engine(head_dim=head_dim))
+    assert be.head_dim == head_dim
+
+
+def test_fp8_pool_at_head_dim_64_is_refused():
+    eng = _engine(head_dim=64, kv_dtype=torch.float8_e4m3fn)
+    with pytest.raises(NotImplementedError, match="fp8"):
         _backend(eng)
 
 

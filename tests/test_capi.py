@@ -125,7 +125,8 @@ def _extend_args(**over):
 
 
 @pytest.mark.parametrize("over,msg", [
-    ({"dim": 64}, "head_dim"),
+    ({"dim": 96}, "head_dim"),
+    ({"dim": 64, "kvdt": 2}, "fp8 KV at head_dim 64"),
     ({"qdt": 3}, "q dtype"),
     ({"kvdt": 0}, "16-bit KV dtype must equal"),
     ({"hq": 12, "hkv": 8}, "head counts"),
@@ -149,9 +150,10 @@ def test_extend_of_nothing_is_a_no_op(lib):
 
 
 def test_extend_workspace_covers_every_row_tile(lib):
-    # 256-row tiles: sum over sequences of ceil(E_b * G / 256) <= ceil(T * G / 256) + B
-    assert lib.ma_extend_workspace_bytes(1000, 40, 8, 3) == 256
-    assert lib.ma_extend_workspace_bytes(100000, 64, 8, 300) == ((3125 + 300) * 8 + 255) // 256 * 256
+    # sized for the smallest row tile (128 rows, head dim 256), which covers every head dim:
+    # sum over sequences of ceil(E_b * G / 128) <= ceil(T * G / 128) + B
+    assert lib.ma_extend_workspace_bytes(1000, 40, 8, 3) == ((40 + 3) * 8 + 255) // 256 * 256
+    assert lib.ma_extend_workspace_bytes(100000, 64, 8, 300) == ((6250 + 300) * 8 + 255) // 256 * 256
     assert lib.ma_extend_workspace_bytes(10, 12, 8, 1) == 0
 
 

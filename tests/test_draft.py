@@ -102,7 +102,7 @@ LAYERS = [fakes.Layer(8, 2)]
     ({"sliding_window_size": 512}, {}, (0, 0), LAYERS, "draft_sliding_window"),
     ({"kv_index_translator": SimpleNamespace(is_translating=True)}, {}, (0, 0), LAYERS, "kv_index_translation"),
     ({}, {}, (0, 0), [], "no_attention_layers"),
-    ({}, {}, (0, 0), [fakes.Layer(8, 2, head_dim=64)], "head_dim"),
+    ({}, {}, (0, 0), [fakes.Layer(8, 2, head_dim=96)], "head_dim"),
 ])
 def test_unsupported_reasons(over, env, window, layers, reason):
     got = draft_decode.unsupported_reason(_runner(**over), 1, env=env, draft_window=window, layers=layers)

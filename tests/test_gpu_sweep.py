@@ -6,6 +6,8 @@ none. Slots are a random permutation of a shared pool, and the table rows are
 permuted inside a larger ``req_to_token``. The same case runs through the split-KV
 decode (the last token of each sequence), the split-KV verify (up to 16 rows per
 sequence) and the MFMA extend (any number of rows). The sizes keep the oracle fast.
+The head dim is 128 except in the ``headdim`` cases, which run 64 and 256 (fp8 pools
+at 64 only through the split-KV kernels, as the extend kernel refuses them).
 """
 
 from __future__ import annotations
@@ -29,12 +31,14 @@ def _ops():
     return ops
 
 
-def _case(seed, max_q):
+def _case(seed, max_q, dim=128, fp8=True):
     g = np.random.default_rng(seed)
     B = int(g.integers(1, 7))
     hkv = int(g.choice([1, 2, 4, 8]))
     G = int(g.choice([1, 2, 3, 5, 8]))
     kv = KV[int(g.integers(0, len(KV)))]
+    if not fp8 and kv in KV[2:]:
+        kv = KV[0] if kv == KV[2] else KV[1]
     q_dtype = torch.float16 if kv == torch.float16 else (torch.bfloat16 if kv == torch.bfloat16 else
                                                          (torch.float16 if g.random() < 0.3 else torch.bfloat16))
     prefix = [int(x) for x in g.integers(0, 700, B)]
@@ -47,20 +51,20 @@ def _case(seed, max_q):
     return B, hkv, G, kv, q_dtype, prefix, ext, causal, window, k_scale, v_scale
 
 
-def _build(seed, max_q):
-    B, hkv, G, kv, q_dtype, prefix, ext, causal, window, ks, vs = _case(seed, max_q)
+def _build(seed, max_q, dim=128, fp8=True):
+    B, hkv, G, kv, q_dtype, prefix, ext, causal, window, ks, vs = _case(seed, max_q, dim, fp8)
     gen = torch.Generator().manual_seed(seed)
     seq = [p + e for p, e in zip(prefix, ext)]
     pool = sum(seq) + 64
-    kf = torch.randn(pool, hkv, 128, generator=gen)
-    vf = torch.randn(pool, hkv, 128, generator=gen)
+    kf = torch.randn(pool, hkv, dim, generator=gen)
+    vf = torch.randn(pool, hkv, dim, generator=gen)
     if kv in KV[2:]:
         k = (kf / ks).to(kv)
         v = (vf / vs).to(kv)
     else:
         k, v = kf.to(kv), vf.to(kv)
     T = sum(ext)
-    q = torch.randn(T, hkv * G, 128, generator=gen).to(q_dtype)
+    q = torch.randn(T, hkv * G, dim, generator=gen).to(q_dtype)
     perm = torch.randperm(pool - 1, generator=gen) + 1
     rows = torch.randperm(B + 3, generator=gen)[:B]
     r2t = torch.zeros(B + 3, max(seq) + 5, dtype=torch.int32)
@@ -70,8 +74,8 @@ def _build(seed, max_q):
         off += n
     qsl = [0] + list(np.cumsum(ext))
     case = dict(q=q, k=k, v=v, r2t=r2t, rows=rows, seq=seq, prefix=prefix, ext=ext, qsl=qsl, causal=causal,
-                window=window, ks=ks, vs=vs, scale=128 ** -0.5)
-    print(f"[case] seed={seed} B={B} hkv={hkv} G={G} kv={kv} q={q_dtype} prefix={prefix} ext={ext} "
+                window=window, ks=ks, vs=vs, scale=dim ** -0.5)
+    print(f"[case] seed={seed} D={dim} B={B} hkv={hkv} G={G} kv={kv} q={q_dtype} prefix={prefix} ext={ext} "
           f"causal={causal} window={window}", flush=True)
     return case
 
@@ -94,43 +98,81 @@ def _device(c):
     return d
 
 
-@pytest.mark.parametrize("seed", range(12))
-def test_sweep_extend(seed):
-    c = _build(1000 + seed, max_q=200)
+def _run_extend(c):
     d = _device(c)
     out = _ops().paged_extend_forward(
         d["q"], d["k"], d["v"], d["r2t"], d["seq"], d["qsl"], d["pre"], softmax_scale=c["scale"],
         k_scale=c["ks"], v_scale=c["vs"], causal=c["causal"], sliding_window_size=c["window"], row_index=d["rows"])
     torch.cuda.synchronize()
-    assert_attn_close(out, _reference(c), what=f"extend seed {seed}")
+    return out
 
 
-@pytest.mark.parametrize("seed", range(12))
-def test_sweep_verify(seed):
-    c = _build(2000 + seed, max_q=16)
+def _run_verify(c):
     d = _device(c)
     out = _ops().paged_verify_forward(
         d["q"], d["k"], d["v"], d["r2t"], d["seq"], d["qsl"], d["pre"], max_q_per_seq=max(max(c["ext"]), 1),
         softmax_scale=c["scale"], k_scale=c["ks"], v_scale=c["vs"], causal=c["causal"],
         sliding_window_size=c["window"], row_index=d["rows"])
     torch.cuda.synchronize()
-    assert_attn_close(out, _reference(c), what=f"verify seed {seed}")
+    return out
 
 
-@pytest.mark.parametrize("seed", range(12))
-def test_sweep_decode(seed):
-    c = _build(3000 + seed, max_q=1)
+def _decode_case(seed, dim=128):
+    c = _build(seed, max_q=1, dim=dim)
     # one query row per sequence, at its last position; empty sequences return zeros
     ctx = c["seq"]
     B, hq = len(ctx), c["q"].shape[1]
-    gen = torch.Generator().manual_seed(3000 + seed)
-    c["q"] = torch.randn(B, hq, 128, generator=gen).to(c["q"].dtype)
+    gen = torch.Generator().manual_seed(seed)
+    c["q"] = torch.randn(B, hq, dim, generator=gen).to(c["q"].dtype)
     c["qsl"] = list(range(B + 1))
     c["prefix"] = [max(n - 1, 0) for n in ctx]
     c["causal"] = True
+    return c
+
+
+def _run_decode(c):
     d = _device(c)
     out = _ops().grouped_decode_forward(
         d["q"], d["k"], d["v"], d["r2t"], d["seq"], softmax_scale=c["scale"], k_scale=c["ks"], v_scale=c["vs"],
         row_index=d["rows"], sliding_window_size=c["window"])
     torch.cuda.synchronize()
-    assert_attn_close(out, _reference(c), what=f"decode seed {seed}")
+    return out
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_extend(seed):
+    c = _build(1000 + seed, max_q=200)
+    assert_attn_close(_run_extend(c), _reference(c), what=f"extend seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_verify(seed):
+    c = _build(2000 + seed, max_q=16)
+    assert_attn_close(_run_verify(c), _reference(c), what=f"verify seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_decode(seed):
+    c = _decode_case(3000 + seed)
+    assert_attn_close(_run_decode(c), _reference(c), what=f"decode seed {seed}")
+
+
+@pytest.mark.parametrize("dim", [64, 256])
+@pytest.mark.parametrize("seed", range(6))
+def test_sweep_headdim_extend(dim, seed):
+    c = _build(4000 + seed, max_q=200, dim=dim, fp8=dim != 64)
+    assert_attn_close(_run_extend(c), _reference(c), what=f"extend D={dim} seed {seed}")
+
+
+@pytest.mark.parametrize("dim", [64, 256])
+@pytest.mark.parametrize("seed", range(6))
+def test_sweep_headdim_verify(dim, seed):
+    c = _build(5000 + seed, max_q=16, dim=dim)
+    assert_attn_close(_run_verify(c), _reference(c), what=f"verify D={dim} seed {seed}")
+
+
+@pytest.mark.parametrize("dim", [64, 256])
+@pytest.mark.parametrize("seed", range(6))
+def test_sweep_headdim_decode(dim, seed):
+    c = _decode_case(6000 + seed, dim=dim)
+    assert_attn_close(_run_decode(c), _reference(c), what=f"decode D={dim} seed {seed}")
