@@ -110,13 +110,13 @@ def _synthetic(gpu, prefix, extend, heads, heads_kv, dtype=torch.bfloat16, page_
 
 
 def _run_synthetic(gpu, prefix, extend, heads, heads_kv, causal=True, window=-1, dtype=torch.bfloat16,
-                   page_size=1, scale=None):
-    q, k, v, table, seq, qsl = _synthetic(gpu, prefix, extend, heads, heads_kv, dtype, page_size)
-    scale = scale or 128 ** -0.5
+                   page_size=1, scale=None, dim=128):
+    q, k, v, table, seq, qsl = _synthetic(gpu, prefix, extend, heads, heads_kv, dtype, page_size, dim=dim)
+    scale = scale or dim ** -0.5
     kc, vc = k, v
     if page_size > 1:
-        kc = k.view(-1, page_size, heads_kv, 128)
-        vc = v.view(-1, page_size, heads_kv, 128)
+        kc = k.view(-1, page_size, heads_kv, dim)
+        vc = v.view(-1, page_size, heads_kv, dim)
     out = _ops().paged_forward(
         q, kc, vc, table.to(gpu), torch.tensor(seq, dtype=torch.int32, device=gpu),
         torch.tensor(qsl, dtype=torch.int32, device=gpu), torch.tensor(prefix, dtype=torch.int32, device=gpu),
@@ -157,6 +157,15 @@ def test_extend_fp16(gpu):
 def test_extend_page_size_16_table(gpu):
     """Reference layout [pages, 16, Hkv, D] with scattered pages (tests/test_attention_v100_gpu.py shapes)."""
     _run_synthetic(gpu, [64, 0], [32, 48], 8, 2, dtype=torch.float16, page_size=16)
+
+
+@pytest.mark.parametrize("prefix,extend", [(64, 32), (0, 48)])
+def test_extend_reference_gpu_test_shape(gpu, prefix, extend):
+    """The reference's own extend GPU test at its exact shape: H4 / Hkv2, D=256, fp16,
+    16-token pages, prefix 64 + 32 and 0 + 48 new tokens
+    (tests/test_attention_v100_gpu.py:49-95). Its pages are in order; here they are
+    scattered."""
+    _run_synthetic(gpu, [prefix], [extend], 4, 2, dtype=torch.float16, page_size=16, dim=256)
 
 
 def test_extend_ragged_batch_with_empty_sequences(gpu):
