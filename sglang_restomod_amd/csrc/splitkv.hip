@@ -731,17 +731,26 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one workgroup per partial-kernel wave W. If W's first piece ended a shared
-// segment, combine the pieces of waves w1..W into the output: a running maximum of the
-// log2 LSEs rescales the sum of the normalised partial outputs, so one pass reads each
-// piece once and the loads of successive pieces do not wait for each other's math.
-// 256 threads cover 1024 / D rows x D head-dim entries per pass.
+// Merge: one workgroup per partial-kernel wave W (for 32-row groups, one per 8-row set of
+// W's row group). If W's first piece ended a shared segment, combine the pieces of waves
+// w1..W into the output: a running maximum of the log2 LSEs rescales the sum of the
+// normalised partial outputs, so one pass reads each piece once and the loads of
+// successive pieces do not wait for each other's math. 256 threads cover 1024 / D rows x
+// D head-dim entries per pass.
 // ---------------------------------------------------------------------------
+// Merge workgroups per partial-kernel wave: one per 8-row set of a 32-row group.
+template <int D, int NB>
+constexpr int merge_split() {
+  return NB == 1 ? 1 : (16 * NB) / (1024 / D);
+}
+
 template <int D, int NB, bool QBF16>
 __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
   const SplitKVArgs a = args;
   constexpr int kRows = 16 * NB;
-  const int W = blockIdx.x;
+  constexpr int kSplit = merge_split<D, NB>();  // workgroups per partial-kernel wave
+  const int W = blockIdx.x / kSplit;
+  const int part = blockIdx.x - W * kSplit;
   const int MA_CONST* dsc = cptr(a.desc) + (int64_t)W * kDescInts;
   if (dsc[0] == 0) return;
   const int b = dsc[1], h = dsc[2], rg = dsc[3], w1 = dsc[4], sel1 = dsc[5];
@@ -752,16 +761,18 @@ __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
   constexpr int kRPP = 256 / kTPR;  // rows per pass of the workgroup
   const int d4 = (threadIdx.x % kTPR) * 4;
   const int r_base = threadIdx.x / kTPR;
-  // thread: rows r_base + kRPP i, head-dim entries d4..d4+3, taken kChunk row sets at a
-  // time; within a chunk the pieces are the outer loop (unrolled by four), so the loads
-  // of a chunk's rows and of four pieces are in flight together. Measured at D=128: one
-  // chunk of all four row sets for 32-row groups (13 -> 10 us on a verify batch of
-  // 32 x 4 tokens), one row set per chunk for 16-row groups, whose second set is padding
-  // when G = 8 (about 5 us on a decode batch of 64).
+  // thread: rows r_base + kRPP i, head-dim entries d4..d4+3. 16-row groups: one
+  // workgroup takes both row sets, one after the other (the second is padding when G = 8).
+  // 32-row groups: each row set has a workgroup of its own. Within a row set the pieces
+  // are the outer loop (unrolled by four), so the loads of four pieces are in flight
+  // together. Measured at D=128 on a verify batch of 32 x 4 tokens: 13 us with one row
+  // set at a time in one workgroup, 10 us with all four together, 8.0 us with a
+  // workgroup per row set; about 5 us on a decode batch of 64.
   constexpr int kPass = kRows / kRPP > 0 ? kRows / kRPP : 1;
-  constexpr int kChunk = (NB == 1) ? 1 : kPass;
+  constexpr int kChunk = 1;
+  static_assert(kSplit == 1 || kSplit == kPass, "a split workgroup takes one row set");
 #pragma unroll
-  for (int c0 = 0; c0 < kPass; c0 += kChunk) {
+  for (int c0 = kSplit == 1 ? 0 : part; c0 < (kSplit == 1 ? kPass : part + 1); c0 += kChunk) {
     bool live = false;  // rows past the last query token (GQA padding) are not read
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
@@ -838,8 +849,9 @@ static hipError_t launch_partial_d(int nb, bool qbf16, int kv, dim3 grid, hipStr
 }
 
 template <int D>
-static hipError_t launch_merge_d(int nb, bool qbf16, dim3 grid, hipStream_t st, const SplitKVArgs& a) {
+static hipError_t launch_merge_d(int nb, bool qbf16, int nwaves, hipStream_t st, const SplitKVArgs& a) {
   constexpr int NB2 = kMaxNB<D>;
+  const dim3 grid((unsigned)(nwaves * (nb == 1 ? merge_split<D, 1>() : merge_split<D, NB2>())));
   if (qbf16) {
     if (nb == 1) hipLaunchKernelGGL((splitkv_merge<D, 1, true>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((splitkv_merge<D, NB2, true>), grid, dim3(256), 0, st, a);
@@ -930,10 +942,9 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
                  : head_dim == 128 ? launch_partial_d<128>(nb, qbf16, kv_dtype, grid, stream, a)
                                    : launch_partial_d<256>(nb, qbf16, kv_dtype, grid, stream, a);
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "split-KV launch failed: %s", hipGetErrorString(e));
-  const dim3 mgrid((unsigned)a.nwaves);  // one workgroup per partial-kernel wave
-  e = head_dim == 64    ? launch_merge_d<64>(nb, qbf16, mgrid, stream, a)
-      : head_dim == 128 ? launch_merge_d<128>(nb, qbf16, mgrid, stream, a)
-                        : launch_merge_d<256>(nb, qbf16, mgrid, stream, a);
+  e = head_dim == 64    ? launch_merge_d<64>(nb, qbf16, a.nwaves, stream, a)
+      : head_dim == 128 ? launch_merge_d<128>(nb, qbf16, a.nwaves, stream, a)
+                        : launch_merge_d<256>(nb, qbf16, a.nwaves, stream, a);
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "merge launch failed: %s", hipGetErrorString(e));
   return MA_OK;
 }
