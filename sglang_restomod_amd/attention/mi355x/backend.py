@@ -255,7 +255,7 @@ class MI355XAttnBackend(_EngineBase):
 
     def _workspace_for(self, mode: str, num_tokens: int, hq: int, hkv: int, batch: int) -> torch.Tensor:
         """The split-KV workspace, which also holds an extend call's work list (8 bytes
-        per 256-row tile); a larger buffer only for a batch whose list does not fit."""
+        per row tile); a larger buffer only for a batch whose list does not fit."""
         ws = self.splitkv_workspace()
         if mode == MODE_VERIFY:
             return ws

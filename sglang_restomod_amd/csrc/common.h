@@ -90,6 +90,24 @@ __device__ __forceinline__ float max3f(float x, float y, float z) {
   return r;
 }
 
+// Maximum of N scores by three-input maxima.
+template <int N>
+__device__ __forceinline__ float max_tree(const float* v) {
+  if constexpr (N == 1) {
+    return v[0];
+  } else if constexpr (N == 2) {
+    return max3f(v[0], v[1], -INFINITY);
+  } else {
+    constexpr int M = (N + 2) / 3;
+    float w[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+      w[i] = 3 * i + 2 < N ? max3f(v[3 * i], v[3 * i + 1], v[3 * i + 2])
+                           : (3 * i + 1 < N ? max3f(v[3 * i], v[3 * i + 1], -INFINITY) : v[3 * i]);
+    return max_tree<M>(w);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // fp8 -> 16-bit, two values per instruction (exact: every e4m3fn / e5m2 value is
 // representable in both fp16 and bf16). `w` holds four fp8 bytes; `hi` selects

@@ -232,25 +232,6 @@ __global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const Exte
   for (int i = m + tid; i < a.capacity; i += kPlanThreads) items[i] = row_tile_item(-1, -1);
 }
 
-// maximum of N values by three-input maxima (which also skip the quieting v_max that
-// the compiler puts on MFMA results)
-template <int N>
-__device__ __forceinline__ float max_tree(const float* v) {
-  if constexpr (N == 1) {
-    return v[0];
-  } else if constexpr (N == 2) {
-    return max3f(v[0], v[1], -INFINITY);
-  } else {
-    constexpr int M = (N + 2) / 3;
-    float w[M];
-#pragma unroll
-    for (int i = 0; i < M; ++i)
-      w[i] = 3 * i + 2 < N ? max3f(v[3 * i], v[3 * i + 1], v[3 * i + 2])
-                           : (3 * i + 1 < N ? max3f(v[3 * i], v[3 * i + 1], -INFINITY) : v[3 * i]);
-    return max_tree<M>(w);
-  }
-}
-
 template <int D, bool QBF16, int KV>
 __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArgs args) {
   const ExtendArgs a = args;  // local copy: the lambdas capture by reference

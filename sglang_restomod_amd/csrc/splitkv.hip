@@ -6,9 +6,9 @@
 // grouped verify partial + combine (_kernels_paged_verify.py:52-433).
 //
 // Work decomposition (stream-K): the key axis of every (sequence, kv head, row group)
-// "segment" is cut into 32-token tiles. All tiles of all segments form one list, and a
-// persistent grid (one 4-wave workgroup per CU) hands every wave an equal, contiguous
-// range of that list. A wave walks its range, keeps an online-softmax state per segment
+// "segment" is cut into 32-token tiles (16 for 16-bit KV at D = 256). All tiles of all
+// segments form one list, and a persistent grid (one 4-wave workgroup per CU) hands
+// every wave an equal, contiguous range of that list. A wave walks its range, keeps an online-softmax state per segment
 // piece, writes the output directly when it covered a whole segment and a partial
 // (normalised O + log2 LSE) when the segment continues in a neighbouring wave's range.
 // Every wave gets at least kMinTiles tiles (small problems use fewer waves), so a segment
@@ -57,8 +57,15 @@
 namespace ma {
 
 constexpr int kWaves = 4;
-constexpr int kTile = 32;
 constexpr int kMaxRows = 32;  // 16 * NB, NB <= 2
+
+// Keys per tile: 32, and 16 for 16-bit KV at D = 256, whose 32-key tile would take 33 of
+// the 63 vector memory instructions a wave can have outstanding (leaving room for one
+// tile in flight); with 16 keys four stages fit.
+template <int D, bool FP8>
+constexpr int kTileKeys() {
+  return (D == 256 && !FP8) ? 16 : 32;
+}
 constexpr int kMinTiles = 2;  // least tiles per active wave
 constexpr int kDescInts = 8;  // per wave: valid, sequence, kv head, row group, first wave, its slot
 
@@ -77,6 +84,7 @@ struct SplitKVArgs {
   int row_groups;            // row groups per (sequence, kv head) in the largest sequence
   int rows;                  // rows per row group (16 * NB)
   int causal, window;
+  int tile_shift;            // log2 of the keys per tile (see kTileKeys)
   float scale_log2;          // softmax_scale * k_scale * log2(e)
   float v_scale;
   int nwaves;                // waves of the persistent grid
@@ -111,7 +119,7 @@ __device__ __forceinline__ Geom geom(const SplitKVArgs& a, int b) {
   g.lo_min = a.window >= 0 ? max(0, g.prefix - a.window) : 0;
   g.lo_min = min(g.lo_min, g.seq);
   g.span = g.seq - g.lo_min;
-  g.nt = (g.span + kTile - 1) / kTile;
+  g.nt = (g.span + (1 << a.tile_shift) - 1) >> a.tile_shift;
   const int real_rows = max(g.ntok, 0) * a.group;
   g.rg_real = min(a.row_groups, (real_rows + a.rows - 1) / a.rows);
   g.seq_row = a.row_index ? cptr(a.row_index)[b] : (int64_t)b;
@@ -281,15 +289,18 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   constexpr int kElt = kFp8 ? 1 : 2;
   constexpr int kRowB = D * kElt;           // bytes of one head row
   constexpr int kCPR = kRowB / 16;          // 16-byte chunks per row
+  constexpr int kTile = kTileKeys<D, kFp8>();  // keys per tile
+  constexpr int TB = kTile / 16;            // 16-key blocks per tile
+  static_assert(TB == 2 || !kFp8, "fp8 V^T reads assume 32-key tiles");
   constexpr int kStage = kTile * kRowB;     // bytes of one V tile
   constexpr int kVL = kStage / 1024;        // 16-byte V loads per lane per tile
   constexpr int KR = kFp8 ? KK / 2 : KK;    // 16-byte K loads per lane per 16-token block
-  constexpr int OPS = 1 + kVL + 2 * KR;     // vector memory instructions per pipeline step
+  constexpr int OPS = 1 + kVL + TB * KR;    // vector memory instructions per pipeline step
   // Pipeline stages: K of S tiles in a register ring, V of S tiles in an LDS ring. Each
   // step issues OPS vector memory instructions (one slot lookup, the V DMA, the K loads);
   // a wave can have at most 63 outstanding, which bounds S: 4 for 16-bit KV at D=128
-  // (more stages measured no faster), 8 where the counter allows it (fp8, D=64), and 2
-  // for 16-bit KV at D=256, whose 32-token tile takes 33 instructions.
+  // (more stages measured no faster) and at D=256 (16-key tiles), 8 where the counter
+  // allows it (fp8, D=64).
   constexpr int kSMax = 63 / OPS + 1;
   constexpr int S = (kFp8 || D == 64) ? (kSMax < 8 ? kSMax : 8) : (kSMax < 4 ? kSMax : 4);
   constexpr int A = 2 * S - 3;  // slots are looked up A tiles ahead of compute
@@ -337,7 +348,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
 
   // ---- per-tile K register ring (V goes to the LDS ring by DMA) ----
   struct Raw {
-    u32x4 k[2][KR];
+    u32x4 k[TB][KR];
   };
   Raw ring[S];
   int sreg[S];
@@ -351,7 +362,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   // register whose load is still in flight.
   auto load_slot = [&](const Cursor& cu) __attribute__((always_inline)) -> int {
     const int key0 = cu.g.lo_min + cu.tile * kTile;
-    const int pos = min(key0 + (lane & 31), cu.g.seq - 1);
+    const int pos = min(key0 + (lane & (kTile - 1)), cu.g.seq - 1);
     const int32_t MA_GLOBAL* tp =
         gptr(a.tt.table) + cu.g.seq_row * a.tt.stride + (pos >> a.tt.page_shift);
     int page;
@@ -361,7 +372,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   // slot = page << page_shift | offset in page; applied after the load has landed
   auto slot_of = [&](const Cursor& cu, int page) __attribute__((always_inline)) -> int {
     const int key0 = cu.g.lo_min + cu.tile * kTile;
-    const int pos = min(key0 + (lane & 31), cu.g.seq - 1);
+    const int pos = min(key0 + (lane & (kTile - 1)), cu.g.seq - 1);
     return (page << a.tt.page_shift) | (pos & ((1 << a.tt.page_shift) - 1));
   };
 
@@ -382,7 +393,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
     }
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
+    for (int tb = 0; tb < TB; ++tb) {
       const int slot = shfl_i(myslot, tb * 16 + c);
       const unsigned char MA_GLOBAL* kp = kbase + (int64_t)slot * row_bytes + hoff;
 #pragma unroll
@@ -401,7 +412,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   };
   auto touch_k = [&](Raw& r) __attribute__((always_inline)) {
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
+    for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
       for (int x = 0; x < KR; ++x) __asm__ volatile("" : "+a"(r.k[tb][x]));
   };
@@ -517,9 +528,9 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     const int tb0 = cu.g.lo_min + cu.tile * kTile;
     const unsigned char* vt = vring[wave][stage];
     // ---- K operand ----
-    u32x4 kr[2][KK];
+    u32x4 kr[TB][KK];
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
+    for (int tb = 0; tb < TB; ++tb) {
       if constexpr (kFp8) {
 #pragma unroll
         for (int half = 0; half < KK / 2; ++half) cvt16_fp8<KV, QBF16>(r.k[tb][half], kr[tb][2 * half], kr[tb][2 * half + 1]);
@@ -529,11 +540,11 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       }
     }
     // ---- S^T = K Q^T ----
-    f32x4 s[NB][2];
+    f32x4 s[NB][TB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb) {
+      for (int tb = 0; tb < TB; ++tb) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) acc = mfma16t<QBF16>(kr[tb][kk], qv[nb][kk], acc);
@@ -548,16 +559,19 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     for (int nb = 0; nb < NB; ++nb) {
       if (!full) {
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
+        for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int pos = tb0 + tb * 16 + 4 * j + i;
             if (pos < lo_r[nb] || pos >= hi_r[nb]) s[nb][tb][i] = -INFINITY;
           }
       }
-      const f32x4* sr = s[nb];
-      float mx = max3f(max3f(sr[0][0], sr[0][1], sr[0][2]), max3f(sr[0][3], sr[1][0], sr[1][1]),
-                       max3f(sr[1][2], sr[1][3], -INFINITY));
+      float sv[4 * TB];
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[4 * tb + i] = s[nb][tb][i];
+      float mx = max_tree<4 * TB>(sv);
       alpha[nb] = 1.f;
       // fp8 KV (more VALU per tile for the conversions): the exponent base moves only when
       // some row's max has grown by more than 2^kLazyRescale in p, so the cross-lane max
@@ -572,12 +586,15 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
         m_run[nb] = m_new;
       }
       const float msc = ((m_run[nb] == -INFINITY) ? 0.f : m_run[nb]) * a.scale_log2;
+      // P^T of the PV MFMA holds 32 keys; a 16-key tile leaves the upper 16 at zero
       float p[8];
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[4 * tb + i] = __builtin_amdgcn_exp2f(s[nb][tb][i] * a.scale_log2 - msc);
-      const float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        for (int i = 0; i < 4; ++i)
+          p[4 * tb + i] = tb < TB ? __builtin_amdgcn_exp2f(s[nb][tb < TB ? tb : 0][i] * a.scale_log2 - msc) : 0.f;
+      const float ps = TB == 2 ? ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]))
+                               : (p[0] + p[1]) + (p[2] + p[3]);
       l_run[nb] = l_run[nb] * alpha[nb] + ps;
       if constexpr (kSplitP) {
 #pragma unroll
@@ -614,6 +631,11 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
         const int chunk = 2 * db + (cc >> 1);
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
+          if (half >= TB) {  // keys past a 16-key tile: zero, like their P
+            va[2 * half] = 0u;
+            va[2 * half + 1] = 0u;
+            continue;
+          }
           const int t = 16 * half + 4 * j + e;
           const unsigned char* ptr = vt + t * kRowB + ((chunk ^ swz(t)) << 4) + (cc & 1) * 8;
           const u32x2 raw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -921,6 +943,7 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
       ((a.q_stride_head * 2) & 15) || ((a.out_stride_tok * 2) & 7) || ((a.out_stride_head * 2) & 7))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   a.group = a.hq / a.hkv;
+  a.tile_shift = (head_dim == 256 && (kv_dtype == DT_F16 || kv_dtype == DT_BF16)) ? 4 : 5;
   const int rows_total = max_q_per_seq * a.group;
   const int nb = (rows_total <= 16 || head_dim == 256) ? 1 : 2;
   a.rows = 16 * nb;
