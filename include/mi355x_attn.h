@@ -26,10 +26,9 @@
  * (sglang_restomod/attention/v100/tilelang/_paged_adapter.py:658,753-754).
  * Query head h reads kv head h / (num_q_heads / num_kv_heads).
  *
- * Head dims of the attention entry points: 64, 128 or 256 (the reference's paged
- * kernels have configurations for 64, 128, 256 and 512, _kernels_paged.py:398-410).
- * fp8 pools at head_dim 64 are read by the split-KV calls only; ma_paged_extend
- * refuses them. Other head dims return MA_EUNSUPPORTED.
+ * Head dims of the attention entry points: 64, 128 or 256, with every KV dtype (the
+ * reference's paged kernels have configurations for 64, 128, 256 and 512,
+ * _kernels_paged.py:398-410). Other head dims return MA_EUNSUPPORTED.
  */
 #ifndef MI355X_ATTN_H
 #define MI355X_ATTN_H

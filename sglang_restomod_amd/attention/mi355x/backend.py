@@ -11,9 +11,8 @@ What differs by design:
 
 * Every supported layer runs on the HIP kernels: decode, prefix-aware extend,
   linear target verify and draft extend. Nothing is delegated to another backend,
-  and layers the kernels cannot serve (head_dim other than 64, 128 or 256, fp8 KV at
-  head_dim 64, logit soft-capping, attention sinks, cross-attention, tree-shaped
-  verify) raise
+  and layers the kernels cannot serve (head_dim other than 64, 128 or 256, logit
+  soft-capping, attention sinks, cross-attention, tree-shaped verify) raise
   ``NotImplementedError`` naming the reason, instead of running elsewhere.
 * The kernels address SGLang's ``req_to_token`` directly (page size 1,
   ``req_pool_indices`` as the row index), so the metadata is the engine's own
@@ -114,9 +113,6 @@ class MI355XAttnBackend(_EngineBase):
             raise NotImplementedError(
                 f"mi355x_attn serves head_dim {ops.SUPPORTED_HEAD_DIMS} with equal q/k and v dims "
                 f"(model has qk {head_dim}, v {v_head_dim})")
-        if (head_dim not in ops.FP8_EXTEND_HEAD_DIMS and self.kv_cache_dtype is not None
-                and self.kv_cache_dtype in (torch.float8_e4m3fn, torch.float8_e5m2)):
-            raise NotImplementedError(f"mi355x_attn reads fp8 KV at head_dim {ops.FP8_EXTEND_HEAD_DIMS}")
         if self.req_to_token.dtype != torch.int32:
             raise ValueError("req_to_token must be int32")
         self.head_dim = head_dim

@@ -27,9 +27,6 @@ FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 
 VERIFY_MAX_Q_PER_SEQ = 64
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
-# head dims at which the extend kernel also reads fp8 pools (at 64 an fp8 tile is smaller
-# than its DMA blocks)
-FP8_EXTEND_HEAD_DIMS = (128, 256)
 
 _WORKSPACES: dict = {}
 _DEVICE_WORKGROUPS: dict = {}

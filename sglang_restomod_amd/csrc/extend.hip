@@ -236,6 +236,7 @@ template <int D, bool QBF16, int KV>
 __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArgs args) {
   const ExtendArgs a = args;  // local copy: the lambdas capture by reference
   constexpr int kXD = D;
+  constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
   constexpr int kXBN = XShape<D>::BN;
   constexpr int kXRB = XShape<D>::RB;
   constexpr int kXBM = XShape<D>::BM;
@@ -243,16 +244,22 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   constexpr int KB = kXBN / 16;                  // 16-key blocks per tile
   constexpr int DB = D / 16;                     // PV MFMA steps
   constexpr int HF = kXBN / 32;                  // 32-key halves of a tile (PV contraction)
-  constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
   constexpr bool kConvV = (!kFp8) && QBF16;      // bf16 V: converted to fp16 in LDS
   constexpr int kElt = kFp8 ? 1 : 2;
   constexpr int kRowB = kXD * kElt;              // bytes of one K/V row
   constexpr int kKSub = kRowB / 64;              // K DMA blocks (1 KB) per 16-key block
   constexpr int kCPR = kRowB / 16;               // 16-byte chunks per row
   constexpr int kStageB = kXBN * kRowB;          // bytes of the K (or V) part of a tile
-  constexpr int kKBlk = kStageB / 1024 / kXWaves;  // K DMA blocks per wave per tile
-  constexpr int kVBlk = kStageB / 1024 / kXWaves;  // V DMA blocks per wave per tile
-  constexpr int ND = kKBlk + kVBlk;              // DMA instructions per wave per tile
+  // DMA blocks (1 KB) of K, and of V, per tile. Each wave moves an equal share of both;
+  // when a tile has fewer blocks than waves (fp8 at D = 64: 4), half the waves move K
+  // and the other half V, one block each, so every wave issues the same count.
+  constexpr int kTileBlk = kStageB / 1024;
+  constexpr bool kSplitDMA = kTileBlk < kXWaves;
+  static_assert(!kSplitDMA || 2 * kTileBlk == kXWaves, "K and V blocks must cover the waves");
+  static_assert(!kSplitDMA || !kConvV, "the V conversion assumes every wave loaded V");
+  constexpr int kKBlk = kSplitDMA ? 1 : kTileBlk / kXWaves;  // K DMA blocks per moving wave
+  constexpr int kVBlk = kSplitDMA ? 1 : kTileBlk / kXWaves;  // V DMA blocks per moving wave
+  constexpr int ND = kSplitDMA ? 1 : kKBlk + kVBlk;          // DMA instructions per wave per tile
   constexpr int OPS = 1 + ND;                    // plus one slot lookup
   // pipeline stages: 5 x 32 KB for 16-bit KV (all 160 KB of LDS), 8 x 16 KB for fp8
   constexpr int S = kFp8 ? 8 : 5;
@@ -366,30 +373,45 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   auto issue = [&](int myslot, int st) __attribute__((always_inline)) {
     const uint32_t kl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)kring[st];
     const uint32_t vl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)vring[st];
-    // all slot shuffles first, so that their LDS round trips overlap; this wave's K blocks
-    // (kb, sub) = divmod(wave * kKBlk + x, kKSub) all lie in key block kb
-    const int kb_w = (wave * kKBlk) / kKSub;
-    const int kslot = shfl_i(myslot, kb_w * 16 + c);
-    int vslot[kVBlk];
-#pragma unroll
-    for (int x = 0; x < kVBlk; ++x) {
-      const int xb = wave * kVBlk + x;
-      vslot[x] = shfl_i(myslot, (64 / kCPR) * xb + lane / kCPR);
-    }
-    // K: lane l -> key kb_w*16 + (l & 15), 16-byte chunk kKSub*j + sub
-    const unsigned char MA_GLOBAL* kp = kbase + (uint64_t)(uint32_t)kslot * row_bytes32 + head_off;
-#pragma unroll
-    for (int x = 0; x < kKBlk; ++x) {
-      const int blk = wave * kKBlk + x;
-      dma(kp + (kKSub * j + blk % kKSub) * 16, kl + blk * 1024);
-    }
-    // V: rows of this wave's blocks, row-major, 16-byte chunks XOR-swizzled by row
-#pragma unroll
-    for (int x = 0; x < kVBlk; ++x) {
-      const int xb = wave * kVBlk + x;
-      const int tok = (64 / kCPR) * xb + lane / kCPR;
+    if constexpr (kSplitDMA) {
+      // waves below kTileBlk move one K block, the others one V block; the source and
+      // destination are selected, not branched on, so that every wave runs the same
+      // instructions around the in-flight slot registers
+      const bool is_k = wave < kTileBlk;
+      const int xb = is_k ? wave : wave - kTileBlk;
+      const int tok = (64 / kCPR) * xb + lane / kCPR;  // V row of this lane
       const int pos = lane % kCPR;
-      dma(vbase + (uint64_t)(uint32_t)vslot[x] * row_bytes32 + head_off + ((pos ^ swz(tok)) << 4), vl + xb * 1024);
+      const int sl = shfl_i(myslot, is_k ? xb * 16 + c : tok);
+      const unsigned char MA_GLOBAL* row = (is_k ? kbase : vbase) + (uint64_t)(uint32_t)sl * row_bytes32 + head_off;
+      // K: lane l -> key 16 * xb + (l & 15), 16-byte chunk kKSub * j (kKSub = 1)
+      const int chunk = is_k ? kKSub * j : (pos ^ swz(tok));
+      dma(row + chunk * 16, (is_k ? kl : vl) + xb * 1024);
+    } else {
+      // all slot shuffles first, so that their LDS round trips overlap; this wave's K blocks
+      // (kb, sub) = divmod(wave * kKBlk + x, kKSub) all lie in key block kb
+      const int kb_w = (wave * kKBlk) / kKSub;
+      const int kslot = shfl_i(myslot, kb_w * 16 + c);
+      int vslot[kVBlk];
+#pragma unroll
+      for (int x = 0; x < kVBlk; ++x) {
+        const int xb = wave * kVBlk + x;
+        vslot[x] = shfl_i(myslot, (64 / kCPR) * xb + lane / kCPR);
+      }
+      // K: lane l -> key kb_w*16 + (l & 15), 16-byte chunk kKSub*j + sub
+      const unsigned char MA_GLOBAL* kp = kbase + (uint64_t)(uint32_t)kslot * row_bytes32 + head_off;
+#pragma unroll
+      for (int x = 0; x < kKBlk; ++x) {
+        const int blk = wave * kKBlk + x;
+        dma(kp + (kKSub * j + blk % kKSub) * 16, kl + blk * 1024);
+      }
+      // V: rows of this wave's blocks, row-major, 16-byte chunks XOR-swizzled by row
+#pragma unroll
+      for (int x = 0; x < kVBlk; ++x) {
+        const int xb = wave * kVBlk + x;
+        const int tok = (64 / kCPR) * xb + lane / kCPR;
+        const int pos = lane % kCPR;
+        dma(vbase + (uint64_t)(uint32_t)vslot[x] * row_bytes32 + head_off + ((pos ^ swz(tok)) << 4), vl + xb * 1024);
+      }
     }
   };
   auto wait_vm = [&](auto N_) __attribute__((always_inline)) {
@@ -616,17 +638,12 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
 
 template <int D, bool QBF16>
 static hipError_t launch_extend_q(int kv, dim3 grid, hipStream_t st, const ExtendArgs& a) {
-  if constexpr (D > 64) {  // at D = 64 an fp8 tile is too small for one 1 KB block per wave
-    if (kv == DT_E4M3) {
-      hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E4M3>), grid, dim3(kXWaves * 64), 0, st, a);
-      return hipGetLastError();
-    }
-    if (kv == DT_E5M2) {
-      hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E5M2>), grid, dim3(kXWaves * 64), 0, st, a);
-      return hipGetLastError();
-    }
-  }
-  hipLaunchKernelGGL((extend_kernel<D, QBF16, QBF16 ? DT_BF16 : DT_F16>), grid, dim3(kXWaves * 64), 0, st, a);
+  if (kv == DT_E4M3)
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E4M3>), grid, dim3(kXWaves * 64), 0, st, a);
+  else if (kv == DT_E5M2)
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E5M2>), grid, dim3(kXWaves * 64), 0, st, a);
+  else
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, QBF16 ? DT_BF16 : DT_F16>), grid, dim3(kXWaves * 64), 0, st, a);
   return hipGetLastError();
 }
 
@@ -667,8 +684,6 @@ extern "C" int ma_paged_extend(
     void* stream) {
   const int bm = extend_tile_rows(head_dim);
   if (bm == 0) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (64, 128 or 256)", head_dim);
-  if (head_dim == 64 && (kv_dtype == DT_E4M3 || kv_dtype == DT_E5M2))
-    return set_error(MA_EUNSUPPORTED, "fp8 KV at head_dim 64 is not supported");
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
   if (kv_dtype < 0 || kv_dtype > DT_E5M2) return set_error(MA_EINVAL, "kv dtype %d unknown", kv_dtype);
   if ((kv_dtype == DT_F16 || kv_dtype == DT_BF16) && kv_dtype != q_dtype)
@@ -701,7 +716,8 @@ extern "C" int ma_paged_extend(
   ExtendPlanArgs p{};
   p.qsl = query_start_loc; p.seq_lens = seq_lens; p.prefix = prefix_lens;
   p.batch = batch; p.group = group; p.causal = causal ? 1 : 0; p.window = sliding_window < 0 ? -1 : sliding_window;
-  p.tile_rows = bm; p.tile_keys = head_dim == 256 ? XShape<256>::BN : XShape<128>::BN;
+  p.tile_rows = bm;
+  p.tile_keys = head_dim == 256 ? XShape<256>::BN : XShape<128>::BN;
   p.capacity = (int)items; p.items = reinterpret_cast<int64_t*>(workspace);
   hipLaunchKernelGGL(extend_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();

@@ -44,10 +44,9 @@ def test_supported_head_dims_construct(head_dim):
     assert be.head_dim == head_dim
 
 
-def test_fp8_pool_at_head_dim_64_is_refused():
-    eng = _engine(head_dim=64, kv_dtype=torch.float8_e4m3fn)
-    with pytest.raises(NotImplementedError, match="fp8"):
-        _backend(eng)
+def test_fp8_pool_at_head_dim_64_constructs():
+    be = _backend(_engine(head_dim=64, kv_dtype=torch.float8_e4m3fn))
+    assert be.head_dim == 64
 
 
 def test_decode_metadata_uses_req_to_token_in_place():

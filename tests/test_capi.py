@@ -126,7 +126,6 @@ def _extend_args(**over):
 
 @pytest.mark.parametrize("over,msg", [
     ({"dim": 96}, "head_dim"),
-    ({"dim": 64, "kvdt": 2}, "fp8 KV at head_dim 64"),
     ({"qdt": 3}, "q dtype"),
     ({"kvdt": 0}, "16-bit KV dtype must equal"),
     ({"hq": 12, "hkv": 8}, "head counts"),

@@ -6,8 +6,7 @@ none. Slots are a random permutation of a shared pool, and the table rows are
 permuted inside a larger ``req_to_token``. The same case runs through the split-KV
 decode (the last token of each sequence), the split-KV verify (up to 16 rows per
 sequence) and the MFMA extend (any number of rows). The sizes keep the oracle fast.
-The head dim is 128 except in the ``headdim`` cases, which run 64 and 256 (fp8 pools
-at 64 only through the split-KV kernels, as the extend kernel refuses them).
+The head dim is 128 except in the ``headdim`` cases, which run 64 and 256.
 """
 
 from __future__ import annotations
@@ -160,7 +159,7 @@ def test_sweep_decode(seed):
 @pytest.mark.parametrize("dim", [64, 256])
 @pytest.mark.parametrize("seed", range(6))
 def test_sweep_headdim_extend(dim, seed):
-    c = _build(4000 + seed, max_q=200, dim=dim, fp8=dim != 64)
+    c = _build(4000 + seed, max_q=200, dim=dim)
     assert_attn_close(_run_extend(c), _reference(c), what=f"extend D={dim} seed {seed}")
 
 
