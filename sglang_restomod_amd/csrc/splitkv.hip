@@ -84,7 +84,6 @@ struct SplitKVArgs {
   int row_groups;            // row groups per (sequence, kv head) in the largest sequence
   int rows;                  // rows per row group (16 * NB)
   int causal, window;
-  int tile_shift;            // log2 of the keys per tile (see kTileKeys)
   float scale_log2;          // softmax_scale * k_scale * log2(e)
   float v_scale;
   int nwaves;                // waves of the persistent grid
@@ -103,6 +102,8 @@ struct Geom {
 
 // Loads go through the constant address space: with a wave-uniform `b` they become
 // scalar loads (geom_u), with a per-lane `b` vector loads (scan over sequences).
+// TS: log2 of the keys per tile (a constant of the partial kernel, see kTileKeys).
+template <int TS>
 __device__ __forceinline__ Geom geom(const SplitKVArgs& a, int b) {
   Geom g;
   g.b = b;
@@ -119,20 +120,22 @@ __device__ __forceinline__ Geom geom(const SplitKVArgs& a, int b) {
   g.lo_min = a.window >= 0 ? max(0, g.prefix - a.window) : 0;
   g.lo_min = min(g.lo_min, g.seq);
   g.span = g.seq - g.lo_min;
-  g.nt = (g.span + (1 << a.tile_shift) - 1) >> a.tile_shift;
+  g.nt = (g.span + (1 << TS) - 1) / (1 << TS);
   const int real_rows = max(g.ntok, 0) * a.group;
   g.rg_real = min(a.row_groups, (real_rows + a.rows - 1) / a.rows);
   g.seq_row = a.row_index ? cptr(a.row_index)[b] : (int64_t)b;
   return g;
 }
 
+template <int TS>
 __device__ __forceinline__ Geom geom_u(const SplitKVArgs& a, int b) {
-  return geom(a, __builtin_amdgcn_readfirstlane(b));
+  return geom<TS>(a, __builtin_amdgcn_readfirstlane(b));
 }
 
 // tiles of sequence b over all its kv heads and row groups
+template <int TS>
 __device__ __forceinline__ int seq_work(const SplitKVArgs& a, int b) {
-  const Geom g = geom(a, b);
+  const Geom g = geom<TS>(a, b);
   return g.nt * g.rg_real * a.hkv;
 }
 
@@ -143,6 +146,7 @@ __device__ __forceinline__ int shfl_up_i(int v, int delta) {
 }
 
 // Total tiles, and (when t >= 0) the sequence holding global tile t and t's offset in it.
+template <int TS>
 __device__ __forceinline__ void scan_work(const SplitKVArgs& a, int64_t t, int64_t& total, int& b_at, int& off_at) {
   const int lane = lane_id();
   int64_t base = 0;
@@ -150,7 +154,7 @@ __device__ __forceinline__ void scan_work(const SplitKVArgs& a, int64_t t, int64
   off_at = 0;
   for (int b0 = 0; b0 < a.batch; b0 += 64) {
     const int b = b0 + lane;
-    const int w = b < a.batch ? seq_work(a, b) : 0;
+    const int w = b < a.batch ? seq_work<TS>(a, b) : 0;
     int inc = w;
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
@@ -171,9 +175,9 @@ __device__ __forceinline__ void scan_work(const SplitKVArgs& a, int64_t t, int64
 
 // Zeros for every real row of sequence b (a sequence whose rows see no key: no tile
 // covers it).
-template <int D>
+template <int D, int TS>
 __device__ __forceinline__ void write_zero_rows(const SplitKVArgs& a, int b) {
-  const Geom g = geom_u(a, b);
+  const Geom g = geom_u<TS>(a, b);
   const int lane = lane_id();
   const int n = g.ntok * a.hq * (D / 4);
   for (int idx = lane; idx < n; idx += 64) {
@@ -189,7 +193,7 @@ __device__ __forceinline__ void write_zero_rows(const SplitKVArgs& a, int b) {
 
 // Total tiles over all sequences. Wave W also zeroes the rows of the key-less sequences
 // b with b mod nwaves == W.
-template <int D>
+template <int D, int TS>
 __device__ __forceinline__ int64_t scan_total(const SplitKVArgs& a, int W) {
   const int lane = lane_id();
   int64_t base = 0;
@@ -198,7 +202,7 @@ __device__ __forceinline__ int64_t scan_total(const SplitKVArgs& a, int W) {
     int w = 0;
     bool zero = false;
     if (b < a.batch) {
-      const Geom g = geom(a, b);
+      const Geom g = geom<TS>(a, b);
       w = g.nt * g.rg_real * a.hkv;
       zero = g.nt == 0 && g.ntok > 0 && (b % a.nwaves) == W;
     }
@@ -209,7 +213,7 @@ __device__ __forceinline__ int64_t scan_total(const SplitKVArgs& a, int W) {
     while (zm) {
       const int L = __builtin_ctzll(zm);
       zm &= zm - 1;
-      write_zero_rows<D>(a, b0 + L);
+      write_zero_rows<D, TS>(a, b0 + L);
     }
   }
   return base;
@@ -229,8 +233,9 @@ struct Cursor {
   int t;  // wave-local tile number
 };
 
+template <int TS>
 __device__ __forceinline__ void cursor_at(const SplitKVArgs& a, Cursor& c, int b, int off) {
-  c.g = geom_u(a, b);
+  c.g = geom_u<TS>(a, b);
   const int per_seg = c.g.nt;
   const int seg = off / per_seg;
   c.tile = off - seg * per_seg;
@@ -240,6 +245,7 @@ __device__ __forceinline__ void cursor_at(const SplitKVArgs& a, Cursor& c, int b
 }
 
 // Next tile of the range; stays on the last tile once the range is exhausted.
+template <int TS>
 __device__ __forceinline__ void cursor_next(const SplitKVArgs& a, Cursor& c, int count) {
   if (c.t + 1 >= count) return;
   ++c.t;
@@ -252,7 +258,7 @@ __device__ __forceinline__ void cursor_next(const SplitKVArgs& a, Cursor& c, int
   int b = c.g.b;
   do {
     ++b;
-    c.g = geom_u(a, b);
+    c.g = geom_u<TS>(a, b);
   } while (c.g.nt * c.g.rg_real == 0);
 }
 
@@ -291,6 +297,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   constexpr int kCPR = kRowB / 16;          // 16-byte chunks per row
   constexpr int kTile = kTileKeys<D, kFp8>();  // keys per tile
   constexpr int TB = kTile / 16;            // 16-key blocks per tile
+  constexpr int kTS = kTile == 16 ? 4 : 5;  // log2(kTile)
   static_assert(TB == 2 || !kFp8, "fp8 V^T reads assume 32-key tiles");
   constexpr int kStage = kTile * kRowB;     // bytes of one V tile
   constexpr int kVL = kStage / 1024;        // 16-byte V loads per lane per tile
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   const int j = lane >> 4;
   const int W = blockIdx.x * kWaves + wave;
 
-  const int64_t total = scan_total<D>(a, W);
+  const int64_t total = scan_total<D, kTS>(a, W);
   const int nA = active_waves(total, a.nwaves);
   int MA_GLOBAL* my_desc = gptr_mut(a.desc) + (int64_t)W * kDescInts;
   if (W >= nA) {
@@ -331,7 +338,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   int b0, off0;
   {
     int64_t tot_again;
-    scan_work(a, t0, tot_again, b0, off0);
+    scan_work<kTS>(a, t0, tot_again, b0, off0);
   }
 
   const unsigned char MA_GLOBAL* kbase = gptr(reinterpret_cast<const unsigned char*>(a.k));
@@ -566,12 +573,14 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
             if (pos < lo_r[nb] || pos >= hi_r[nb]) s[nb][tb][i] = -INFINITY;
           }
       }
-      float sv[4 * TB];
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv[4 * tb + i] = s[nb][tb][i];
-      float mx = max_tree<4 * TB>(sv);
+      float mx;
+      if constexpr (TB == 2) {
+        const f32x4* sr = s[nb];
+        mx = max3f(max3f(sr[0][0], sr[0][1], sr[0][2]), max3f(sr[0][3], sr[1][0], sr[1][1]),
+                   max3f(sr[1][2], sr[1][3], -INFINITY));
+      } else {
+        mx = max3f(max3f(s[nb][0][0], s[nb][0][1], s[nb][0][2]), s[nb][0][3], -INFINITY);
+      }
       alpha[nb] = 1.f;
       // fp8 KV (more VALU per tile for the conversions): the exponent base moves only when
       // some row's max has grown by more than 2^kLazyRescale in p, so the cross-lane max
@@ -588,13 +597,21 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       const float msc = ((m_run[nb] == -INFINITY) ? 0.f : m_run[nb]) * a.scale_log2;
       // P^T of the PV MFMA holds 32 keys; a 16-key tile leaves the upper 16 at zero
       float p[8];
+      float ps;
+      if constexpr (TB == 2) {
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
+        for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          p[4 * tb + i] = tb < TB ? __builtin_amdgcn_exp2f(s[nb][tb < TB ? tb : 0][i] * a.scale_log2 - msc) : 0.f;
-      const float ps = TB == 2 ? ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]))
-                               : (p[0] + p[1]) + (p[2] + p[3]);
+          for (int i = 0; i < 4; ++i) p[4 * tb + i] = __builtin_amdgcn_exp2f(s[nb][tb][i] * a.scale_log2 - msc);
+        ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = __builtin_amdgcn_exp2f(s[nb][0][i] * a.scale_log2 - msc);
+          p[4 + i] = 0.f;
+        }
+        ps = (p[0] + p[1]) + (p[2] + p[3]);
+      }
       l_run[nb] = l_run[nb] * alpha[nb] + ps;
       if constexpr (kSplitP) {
 #pragma unroll
@@ -657,7 +674,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   // A = 2S-3 is the largest lead the S-entry slot ring allows, and it keeps the wait for a
   // slot register from forcing any tile newer than the one about to be computed.
   Cursor cc, ci, cs;
-  cursor_at(a, cc, b0, off0);
+  cursor_at<kTS>(a, cc, b0, off0);
   ci = cc;
   cs = cc;
   // Schedule. Step n: look up the slots of tile n+A, issue tile n+S-1 (its slots were
@@ -676,7 +693,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     constexpr int N = decltype(N_)::value - A;
     constexpr int SI = ((N + A) % S + S) % S;
     sreg[SI] = load_slot(cs);
-    cursor_next(a, cs, count);
+    cursor_next<kTS>(a, cs, count);
     if constexpr (N + S - 1 >= 0) {
       constexpr int RI = ((N + S - 1) % S + S) % S;
       // the slot lookup of tile N+S-1 was issued at step N+S-1-A, first in its step
@@ -684,7 +701,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       wait_vm(std::integral_constant<int, W>{});
       __asm__ volatile("" : "+v"(sreg[RI]));
       issue(ci, slot_of(ci, sreg[RI]), ring[RI], RI);
-      cursor_next(a, ci, count);
+      cursor_next<kTS>(a, ci, count);
     }
   };
   [&]<int... Is>(std::integer_sequence<int, Is...>) __attribute__((always_inline)) {
@@ -696,12 +713,12 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     constexpr int RI = (I + S - 1) % S;
     // slot of tile n+A -> sreg[(n+A) % S] (that register's previous tile is already issued)
     sreg[(I + A) % S] = load_slot(cs);
-    cursor_next(a, cs, count);
+    cursor_next<kTS>(a, cs, count);
     // K/V of tile n+S-1, once its slot lookup (A-S+1 steps ago) has landed
     wait_vm(std::integral_constant<int, OPS * (A - S + 1)>{});
     __asm__ volatile("" : "+v"(sreg[RI]));
     issue(ci, slot_of(ci, sreg[RI]), ring[RI], RI);
-    cursor_next(a, ci, count);
+    cursor_next<kTS>(a, ci, count);
     if (n < count) {
       if (cc.t == 0 || cc.tile == 0) {
         begin_segment(cc);
@@ -726,7 +743,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
         end_segment(cc, whole, first_piece ? 0 : 1);
         first_piece = false;
       }
-      cursor_next(a, cc, count);
+      cursor_next<kTS>(a, cc, count);
     }
   };
 
@@ -776,7 +793,7 @@ __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
   const int MA_CONST* dsc = cptr(a.desc) + (int64_t)W * kDescInts;
   if (dsc[0] == 0) return;
   const int b = dsc[1], h = dsc[2], rg = dsc[3], w1 = dsc[4], sel1 = dsc[5];
-  const Geom g = geom_u(a, b);
+  const Geom g = geom_u<5>(a, b);  // only its token range is read here, not the tile count
   const float MA_GLOBAL* plse = gptr(a.part_lse);
   const float MA_GLOBAL* po = gptr(a.part_o);
   constexpr int kTPR = D / 4;       // threads per row, four head-dim entries each
@@ -943,7 +960,6 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
       ((a.q_stride_head * 2) & 15) || ((a.out_stride_tok * 2) & 7) || ((a.out_stride_head * 2) & 7))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   a.group = a.hq / a.hkv;
-  a.tile_shift = (head_dim == 256 && (kv_dtype == DT_F16 || kv_dtype == DT_BF16)) ? 4 : 5;
   const int rows_total = max_q_per_seq * a.group;
   const int nb = (rows_total <= 16 || head_dim == 256) ? 1 : 2;
   a.rows = 16 * nb;
