@@ -5,10 +5,12 @@
 // _paged_adapter.py:567-759): query token i of sequence b sees key j when
 //   j < seq_lens[b]  and (causal: j <= prefix[b] + i)  and (window W >= 0: j >= prefix[b] + i - W).
 //
-// Decomposition: one workgroup = 8 waves = 256 query rows of ONE kv head, where row r of
-// a sequence is (query token r / G, GQA head r % G); each wave owns 32 rows (two 16-row
-// blocks), two waves per SIMD so that one's softmax overlaps the other's MFMAs. All G
-// heads that share a kv head are served from one copy of each K/V tile in LDS.
+// Decomposition (head dims 64 and 128; XShape below gives D = 256's): one workgroup =
+// 8 waves = 256 query rows of ONE kv head, where row r of a sequence is (query token
+// r / G, GQA head r % G); each wave owns 32 rows (two 16-row blocks), two waves per SIMD
+// so that one's softmax overlaps the other's MFMAs. All G heads that share a kv head are
+// served from one copy of each K/V tile in LDS. At D = 256 a wave owns 16 rows and a
+// tile has 32 keys.
 //
 // Work list: a one-workgroup plan kernel lists the row tiles (sequence, tile) of the
 // batch from query_start_loc on the device, ordered by their key-tile count, heaviest
@@ -17,7 +19,7 @@
 // head fastest: workgroup i runs on XCD i % 8, so with 8 kv heads each XCD streams one
 // head's K/V through its own L2.
 //
-// Per 64-key tile, per wave (scores of all 64 keys, then one online-softmax update, then
+// Per 64-key tile, per wave (scores of all its keys, then one online-softmax update, then
 // PV), MFMA 16x16x32 with fp32 accumulate; the softmax's VALU work is what bounds the
 // kernel, so the row sums of P also come from an MFMA (a block of V^T whose row 0 is
 // ones), the row max uses three-input maxima, and O is rescaled only when a row's max
@@ -33,9 +35,11 @@
 //
 // Memory pipeline: K and V tiles travel HBM -> LDS by DMA (global_load_lds) into an
 // S-stage ring (5 stages for 16-bit KV, 8 for fp8), with S-1 tiles in flight while one
-// computes; each wave moves an eighth of every tile. K lands as MFMA fragment blocks (block (kb, kk) = 16 keys x 8 head-dim
-// entries, lane l's 16 bytes at l * 16), so each operand read is one conflict-free
-// ds_read_b128; V lands row-major with an XOR swizzle of its 16-byte chunks. Slots are
+// computes; each wave moves an eighth of every tile (for an fp8 tile at D = 64, half the
+// waves move K and half V). K lands as MFMA fragment blocks (a 1 KB block holds 16 keys
+// x 16 bytes per lane, lane l's 16 bytes at l * 16), so each operand read is one
+// conflict-free ds_read_b128; V lands row-major with an XOR swizzle of its 16-byte
+// chunks. Slots are
 // looked up S+1 tiles ahead. The loads are inline assembly with explicit wait counts,
 // and one barrier per tile both publishes a tile and retires the stage it replaces.
 
