@@ -21,10 +21,12 @@ def _rand(*shape, seed=0):
     return np.random.default_rng(seed).standard_normal(shape)
 
 
-def test_matches_sdpa_with_causal_prefix_mask():
+@pytest.mark.parametrize("D", [16, 64, 128, 256])
+def test_matches_sdpa_with_causal_prefix_mask(D):
     """Extend vs torch SDPA with an explicit causal-with-prefix mask and GQA repeat
-    (the form of the reference's tests/test_attention_v100_gpu.py:28-46)."""
-    P, E, H, Hkv, D = 37, 11, 8, 2, 16
+    (the form of the reference's tests/test_attention_v100_gpu.py:28-46), at the
+    kernels' head dims too."""
+    P, E, H, Hkv = 37, 11, 8, 2
     n = P + E
     q, k, v = _rand(E, H, D, seed=1), _rand(n, Hkv, D, seed=2), _rand(n, Hkv, D, seed=3)
     out = A.extend(q, k, v, np.arange(n)[None, :], [0], [P], [E], softmax_scale=D ** -0.5)
