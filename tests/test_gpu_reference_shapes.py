@@ -1,10 +1,12 @@
-"""The reference's own grouped-decode GPU test at its exact shapes, against the float64
+"""The reference's own grouped-decode GPU tests at their exact shapes, against the float64
 oracle (tests/test_native_draft_decode_gpu.py:63-135 in the reference): 12 query heads,
 2 kv heads, head dim 256, 16-token pages handed to each row in reverse logical order (so
 that a page-table mistake cannot pass by accident), the page table built from flat
 ``kv_indptr`` / ``kv_indices`` lists, fp16 and e5m2 pools, lengths [37, 53], [67] and
 [41, 67]. The reference checks against SDPA at 2e-2; the bound here is the oracle's
-2e-3 + half an output ulp. The reference's extend GPU test shape runs in
+2e-3 + half an output ulp. The dense e5m2 decode case of
+tests/test_qsa_kernels_gpu.py:233-303 (6 query heads on 1 kv head, lengths [200, 480],
+seeds 40 and 50) runs here too. The reference's extend GPU test shape runs in
 tests/test_gpu_extend.py (test_extend_reference_gpu_test_shape).
 """
 
@@ -68,3 +70,33 @@ def test_grouped_decode_reference_gpu_test_shape(lengths, dtype):
     ref = oracle.paged_attention(to_f64(q), flat_k, flat_v, slots, list(range(len(lengths) + 1)),
                                  [n - 1 for n in lengths], lengths, softmax_scale=scale, causal=True)
     assert_attn_close(out, ref, what=f"grouped decode {lengths} {dtype}")
+
+
+@pytest.mark.parametrize("seed", [40, 50])
+def test_grouped_decode_dense_e5m2_shape(seed):
+    """The reference's dense e5m2 decode case (tests/test_qsa_kernels_gpu.py:233-303):
+    head dim 256, 6 query heads on 1 kv head, e5m2 K and V, 16-token pages, every row's
+    page table a random permutation of the same 32 pages, lengths [200, 480], fp16
+    queries. The reference bound is 3e-3; here the oracle's."""
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    dim, page_size, pages, lengths = 256, 16, 32, [200, 480]
+    print(f"[case] dense e5m2 seed={seed}", flush=True)
+    gen = torch.Generator().manual_seed(seed)
+    k_cache = torch.randn(pages, page_size, 1, dim, generator=gen).to(torch.float8_e5m2)
+    v_cache = torch.randn(pages, page_size, 1, dim, generator=gen).to(torch.float8_e5m2)
+    page_table = torch.stack([torch.randperm(pages, generator=gen) for _ in lengths]).to(torch.int32)
+    q = torch.randn(len(lengths), 6, dim, generator=gen).to(torch.float16)
+    scale = dim ** -0.5
+    out = ops.grouped_decode_forward(q.to(DEV), k_cache.to(DEV), v_cache.to(DEV), page_table.to(DEV),
+                                     torch.tensor(lengths, dtype=torch.int32, device=DEV), softmax_scale=scale)
+    torch.cuda.synchronize()
+
+    flat_k = k_cache.float().reshape(-1, 1, dim).numpy().astype(np.float64)
+    flat_v = v_cache.float().reshape(-1, 1, dim).numpy().astype(np.float64)
+    offs = np.arange(page_size)
+    slots = [(page_table[r, : (n + page_size - 1) // page_size].numpy().astype(np.int64)[:, None] * page_size
+              + offs[None, :]).reshape(-1)[:n] for r, n in enumerate(lengths)]
+    ref = oracle.paged_attention(to_f64(q), flat_k, flat_v, slots, list(range(len(lengths) + 1)),
+                                 [n - 1 for n in lengths], lengths, softmax_scale=scale, causal=True)
+    assert_attn_close(out, ref, what=f"dense e5m2 decode seed {seed}")
