@@ -1,7 +1,7 @@
 """End-to-end through MI355XAttnBackend on the GPU: a serving sequence over the
 fake engine (cached prefix -> extend -> decode -> linear verify -> draft extend)
-for each KV dtype, and decode captured in a HIP graph and replayed with new
-lengths. Every output is checked against the float64 oracle over the pool as the
+for each KV dtype (and at head dims 64 and 256 for bf16 and e4m3), and decode
+captured in a HIP graph and replayed with new lengths. Every output is checked against the float64 oracle over the pool as the
 backend left it (after its own K/V writes)."""
 
 from __future__ import annotations
@@ -26,11 +26,12 @@ def _backend(engine):
     return MI355XAttnBackend(engine.runner)
 
 
-def _layer(kv_dtype):
+def _layer(kv_dtype, hq=HQ, hkv=HKV, dim=D):
+    shape = dict(head_dim=dim, scaling=dim ** -0.5)
     if kv_dtype in fakes.FP8:
-        return fakes.Layer(HQ, HKV, k_scale=torch.tensor(1.5, device=DEV), v_scale=torch.tensor(0.75, device=DEV),
-                           k_scale_float=1.5, v_scale_float=0.75)
-    return fakes.Layer(HQ, HKV)
+        return fakes.Layer(hq, hkv, k_scale=torch.tensor(1.5, device=DEV), v_scale=torch.tensor(0.75, device=DEV),
+                           k_scale_float=1.5, v_scale_float=0.75, **shape)
+    return fakes.Layer(hq, hkv, **shape)
 
 
 def _pools(eng):
@@ -40,25 +41,26 @@ def _pools(eng):
 
 
 def _check_extend(eng, layer, fb, q, out, prefix, ext, what):
+    hq, dim = layer.tp_q_head_num, layer.head_dim
     kp, vp = _pools(eng)
     r2t = eng.req_to_token.cpu().numpy()
     rows = fb.req_pool_indices.tolist()
-    ref = oracle.extend(to_f64(q).reshape(-1, HQ, D), kp, vp, r2t, rows, prefix, ext,
+    ref = oracle.extend(to_f64(q).reshape(-1, hq, dim), kp, vp, r2t, rows, prefix, ext,
                         softmax_scale=layer.scaling, k_scale=layer.k_scale_float, v_scale=layer.v_scale_float)
     assert out.shape == q.shape and out.dtype == q.dtype
-    assert_attn_close(out.reshape(-1, HQ, D), ref, what=what)
+    assert_attn_close(out.reshape(-1, hq, dim), ref, what=what)
 
 
 def _rand(gen, *shape, dtype=torch.bfloat16):
     return torch.randn(*shape, generator=gen).to(dtype).to(DEV)
 
 
-@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float8_e5m2])
-def test_serving_sequence(kv_dtype):
+def _serving_sequence(kv_dtype, HQ=HQ, HKV=HKV, D=D):
+    print(f"[case] serving sequence {kv_dtype} hq={HQ} hkv={HKV} d={D}", flush=True)
     gen = torch.Generator().manual_seed(7)
-    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=kv_dtype, pool_size=12000, max_reqs=6,
+    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, head_dim=D, kv_dtype=kv_dtype, pool_size=12000, max_reqs=6,
                        context_len=4096, spec="EAGLE", topk=1)
-    layer = _layer(kv_dtype)
+    layer = _layer(kv_dtype, HQ, HKV, D)
     be = _backend(eng)
     # cached prefixes computed by earlier forwards
     prefix = {0: 300, 1: 0, 2: 1000}
@@ -101,6 +103,19 @@ def test_serving_sequence(kv_dtype):
     assert be.forward_metadata.mode == "verify"
     out = be.forward_extend(q, k, v, layer, fb)
     _check_extend(eng, layer, fb, q, out, fb.before, [3, 1, 6], f"draft extend {kv_dtype}")
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float8_e5m2])
+def test_serving_sequence(kv_dtype):
+    _serving_sequence(kv_dtype)
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("hq,hkv,dim", [(8, 2, 64), (12, 2, 256)])
+def test_serving_sequence_head_dims(kv_dtype, hq, hkv, dim):
+    """The same sequence at head dims 64 and 256 (the latter with the 27B model's
+    per-GPU head counts)."""
+    _serving_sequence(kv_dtype, hq, hkv, dim)
 
 
 def test_sliding_window_layer_through_swa_pool():
