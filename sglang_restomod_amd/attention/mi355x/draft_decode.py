@@ -53,7 +53,12 @@ class MI355XDraftDecodeBackend(_EngineBase):
         self._row_index: Optional[torch.Tensor] = None
         self._seq_lens: Optional[torch.Tensor] = None
         self._rows_used = 0
+        # the split-KV workspace grows with the head dim: sized for the model's (the
+        # largest supported one when the runner does not say), grown for a wider layer
+        model_config = getattr(model_runner, "model_config", None)
+        self.head_dim = int(getattr(model_config, "head_dim", max(plan.SUPPORTED_HEAD_DIMS)))
         self._workspace: Optional[torch.Tensor] = None
+        self._workspace_dim = 0
         self._graph_rows = 0
 
     # ---- metadata ----
@@ -95,7 +100,8 @@ class MI355XDraftDecodeBackend(_EngineBase):
         self._g_seq_lens = torch.zeros(rows, dtype=torch.int32, device=self.device)
         self._graph_rows = rows
         if self.device.type == "cuda":
-            self._workspace = ops.splitkv_workspace(self.device)
+            self._workspace = ops.splitkv_workspace(self.device, head_dim=self.head_dim)
+            self._workspace_dim = self.head_dim
 
     def get_cuda_graph_seq_len_fill_value(self) -> int:
         return 1
@@ -132,8 +138,9 @@ class MI355XDraftDecodeBackend(_EngineBase):
         if rows:
             ks = float(layer.k_scale_float) if getattr(layer, "k_scale", None) is not None else 1.0
             vs = float(layer.v_scale_float) if getattr(layer, "v_scale", None) is not None else 1.0
-            if self._workspace is None and q3.is_cuda:
-                self._workspace = ops.splitkv_workspace(q3.device)
+            if q3.is_cuda and (self._workspace is None or self._workspace_dim < d):
+                self._workspace = ops.splitkv_workspace(q3.device, head_dim=d)
+                self._workspace_dim = d
             ops.grouped_decode_forward(
                 q3, k_cache, v_cache, self._table, self._seq_lens, softmax_scale=float(layer.scaling),
                 k_scale=ks, v_scale=vs, out=out, row_index=self._row_index, page_size=1,

@@ -1,6 +1,7 @@
 """A draft step on the GPU: split-KV decode over the step's flat kv_indptr /
 kv_indices list (ragged rows, shared prefixes as with top-k branches, an empty row),
-eagerly and from a captured HIP graph, against the float64 oracle."""
+eagerly and from a captured HIP graph, against the float64 oracle, at 16 query heads on 4
+kv heads with D=128 and at the reference draft kernel's layout (6 on 1, D=256)."""
 
 from __future__ import annotations
 
@@ -37,7 +38,8 @@ def _reference(eng, layer, q, rows_tokens):
     vp = to_f64(eng.pool.get_value_buffer(0))
     slots = [np.asarray(t, dtype=np.int64) for t in rows_tokens]
     n = [len(t) for t in rows_tokens]
-    return oracle.paged_attention(to_f64(q).reshape(len(n), HQ, D), kp, vp, slots, list(range(len(n) + 1)),
+    hq, dim = layer.tp_q_head_num, layer.head_dim
+    return oracle.paged_attention(to_f64(q).reshape(len(n), hq, dim), kp, vp, slots, list(range(len(n) + 1)),
                                   [max(x - 1, 0) for x in n], n, softmax_scale=layer.scaling,
                                   k_scale=layer.k_scale_float, v_scale=layer.v_scale_float)
 
@@ -49,11 +51,17 @@ def _step(eng, topk=2):
 
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e5m2])
-def test_draft_step_over_flat_index_lists(kv_dtype):
+@pytest.mark.parametrize("HQ,HKV,D", [(HQ, HKV, D), (6, 1, 256)])
+def test_draft_step_over_flat_index_lists(kv_dtype, HQ, HKV, D):
+    """(6, 1, 256) is the head layout of the reference's draft-decode kernel
+    (sm70_longctx_decode.cu, H6/D256)."""
+    print(f"[case] draft step {kv_dtype} hq={HQ} hkv={HKV} d={D}", flush=True)
     gen = torch.Generator().manual_seed(13)
-    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=kv_dtype, pool_size=6000, max_reqs=4, context_len=4096)
+    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, head_dim=D, kv_dtype=kv_dtype, pool_size=6000, max_reqs=4,
+                       context_len=4096)
+    shape = dict(head_dim=D, scaling=D ** -0.5)
     layer = (fakes.Layer(HQ, HKV, k_scale=torch.tensor(1.25), v_scale=torch.tensor(0.5), k_scale_float=1.25,
-                         v_scale_float=0.5) if kv_dtype != torch.bfloat16 else fakes.Layer(HQ, HKV))
+                         v_scale_float=0.5, **shape) if kv_dtype != torch.bfloat16 else fakes.Layer(HQ, HKV, **shape))
     prefix = {}
     for r, n in ((0, 900), (1, 37), (2, 2000)):
         s = eng.alloc(r, n)
@@ -82,10 +90,13 @@ def test_draft_step_over_flat_index_lists(kv_dtype):
     del rows_with_token
 
 
-def test_draft_step_in_a_hip_graph():
+@pytest.mark.parametrize("HQ,HKV,D", [(HQ, HKV, D), (6, 1, 256)])
+def test_draft_step_in_a_hip_graph(HQ, HKV, D):
     gen = torch.Generator().manual_seed(17)
-    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=torch.bfloat16, pool_size=6000, max_reqs=4, context_len=4096)
-    layer = fakes.Layer(HQ, HKV)
+    print(f"[case] draft graph hq={HQ} hkv={HKV} d={D}", flush=True)
+    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, head_dim=D, kv_dtype=torch.bfloat16, pool_size=6000, max_reqs=4,
+                       context_len=4096)
+    layer = fakes.Layer(HQ, HKV, head_dim=D, scaling=D ** -0.5)
     base = {}
     for r, n in ((0, 300), (1, 1200)):
         s = eng.alloc(r, n)
