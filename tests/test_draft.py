@@ -8,7 +8,7 @@ from types import SimpleNamespace
 import pytest
 import torch
 
-from sglang_restomod_amd.attention.mi355x import draft_backend, draft_decode
+from sglang_restomod_amd.attention.mi355x import draft_backend, draft_decode, draft_decode_plan
 from tests import fakes
 
 
@@ -177,6 +177,17 @@ def test_step_metadata_in_graph_buffers_keeps_addresses():
     assert step._seq_lens.tolist() == [1, 1]
     with pytest.raises(ValueError, match="capacity"):
         step.refresh(torch.arange(7, dtype=torch.int32), torch.arange(6, dtype=torch.int32))
+
+
+def test_step_sizes_its_workspace_for_the_model_head_dim():
+    """The split-KV workspace grows with the head dim, so a step takes the model's
+    (and the largest supported one when the runner gives no model config)."""
+    runner = _runner()
+    runner.model_config.head_dim = 256
+    assert draft_decode.MI355XDraftDecodeBackend(runner, 1, 2048, 1, 3).head_dim == 256
+    bare = SimpleNamespace(**{k: v for k, v in vars(_runner()).items() if k != "model_config"})
+    step = draft_decode.MI355XDraftDecodeBackend(bare, 1, 2048, 1, 3)
+    assert step.head_dim == max(draft_decode_plan.SUPPORTED_HEAD_DIMS)
 
 
 def test_step_refuses_mismatched_rows():
