@@ -117,7 +117,8 @@ def quantize(bits: np.ndarray, src: str, dst: str, scale: Optional[float]) -> np
             return to_fp8(vals, dst)
     if dst == "bf16":
         return f32_to_bf16(vals)
-    return vals.astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):  # beyond fp16's range rounds to inf, as the kernel does
+        return vals.astype(np.float16).view(np.uint16)
 
 
 def set_kv_buffer(cache: np.ndarray, loc: np.ndarray, src_bits: np.ndarray, src: str, dst: str,
