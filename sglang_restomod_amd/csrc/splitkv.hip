@@ -288,7 +288,6 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
   constexpr int KK = D / 32;          // QK MFMA steps
   constexpr int DB = D / 16;          // PV MFMA steps
-  constexpr int DQ = D / 4;           // head-dim entries per lane group in QK
   constexpr int kRows = 16 * NB;
   constexpr bool kPvBf16 = (!kFp8) && QBF16;
   constexpr bool kSplitP = kPvBf16;
@@ -321,6 +320,14 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   const int c = lane & 15;
   const int j = lane >> 4;
   const int W = blockIdx.x * kWaves + wave;
+  // Head-dim order of the QK contraction. K load x of a lane (c, j) reads bytes
+  // x*64 + j*16 .. +16 of its token's row, so each load instruction reads 64 contiguous
+  // bytes of 16 rows; MFMA step kk then holds dims qdim(kk) .. +8 of lane group j, and
+  // the query rows are loaded in the same order.
+  auto qdim = [&](int kk) -> int {
+    if constexpr (kFp8) return (kk >> 1) * 64 + j * 16 + (kk & 1) * 8;
+    else return kk * 32 + j * 8;
+  };
 
   const int64_t total = scan_total<D, kTS>(a, W);
   const int nA = active_waves(total, a.nwaves);
@@ -373,7 +380,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     const int32_t MA_GLOBAL* tp =
         gptr(a.tt.table) + cu.g.seq_row * a.tt.stride + (pos >> a.tt.page_shift);
     int page;
-    __asm__ volatile("global_load_dword %0, %1, off" : "=v"(page) : "v"(tp) : "memory");
+    __asm__ volatile("global_load_dword %0, %1, off" MA_SLOT_POLICY : "=v"(page) : "v"(tp) : "memory");
     return page;
   };
   // slot = page << page_shift | offset in page; applied after the load has landed
@@ -397,7 +404,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       const int slot = shfl_i(myslot, tok);
       const unsigned char MA_GLOBAL* src = vbase + (int64_t)slot * row_bytes + hoff + ((pos ^ swz(tok)) << 4);
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + x * 1024);
-      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" MA_V_POLICY : : "s"(m0), "v"(src) : "memory", "m0");
     }
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
@@ -405,8 +412,8 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       const unsigned char MA_GLOBAL* kp = kbase + (int64_t)slot * row_bytes + hoff;
 #pragma unroll
       for (int x = 0; x < KR; ++x) {
-        const int off = kFp8 ? (j * DQ + x * 16) : (j * DQ + x * 8) * 2;
-        __asm__ volatile("global_load_dwordx4 %0, %1, off" : "=a"(r.k[tb][x]) : "v"(kp + off) : "memory");
+        const int off = x * 64 + j * 16;  // 64 contiguous bytes of the row per instruction
+        __asm__ volatile("global_load_dwordx4 %0, %1, off" MA_K_POLICY : "=a"(r.k[tb][x]) : "v"(kp + off) : "memory");
       }
     }
   };
@@ -463,10 +470,10 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       const int tq = real[nb] ? t : 0;
       const int gq = real[nb] ? g : 0;
       const uint16_t MA_GLOBAL* qp = qbase + (int64_t)(cu.g.tok0 + tq) * a.q_stride_tok +
-                                     (int64_t)(cu.h * a.group + gq) * a.q_stride_head + j * DQ;
+                                     (int64_t)(cu.h * a.group + gq) * a.q_stride_head;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
-        __asm__ volatile("global_load_dwordx4 %0, %1, off" : "=v"(qv[nb][kk]) : "v"(qp + kk * 8) : "memory");
+        __asm__ volatile("global_load_dwordx4 %0, %1, off" : "=v"(qv[nb][kk]) : "v"(qp + qdim(kk)) : "memory");
       m_run[nb] = -INFINITY;
       l_run[nb] = 0.f;
 #pragma unroll
