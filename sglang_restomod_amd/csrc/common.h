@@ -44,8 +44,7 @@ __device__ __forceinline__ const T MA_CONST* cptr(const T* p) {
 }
 
 // Cache policies of the inline-assembly loads of decode and verify (appended to the
-// mnemonic). V rows (DMA to LDS, whole rows per instruction) stream with the
-// nontemporal hint: on random-slot gathers of 256-byte and 2 KiB rows, nt loads of whole
+// mnemonic). K and V rows (whole rows per instruction) stream with the nontemporal hint: on random-slot gathers of 256-byte and 2 KiB rows, nt loads of whole
 // rows reach 6.4-6.5 TB/s against 5.7-5.8 TB/s for default-policy loads, sequential or
 // random alike. Slot lookups keep the default policy (each (sequence, kv head) segment
 // re-reads its sequence's slots).
@@ -53,7 +52,7 @@ __device__ __forceinline__ const T MA_CONST* cptr(const T* p) {
 #define MA_V_POLICY " nt"
 #endif
 #ifndef MA_K_POLICY
-#define MA_K_POLICY ""
+#define MA_K_POLICY " nt"
 #endif
 #ifndef MA_SLOT_POLICY
 #define MA_SLOT_POLICY ""

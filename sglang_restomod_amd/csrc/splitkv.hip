@@ -39,9 +39,11 @@
 //
 // Memory pipeline: K and V of the next S-1 tiles are in flight while a tile computes
 // (at D = 128, S = 4 for 16-bit KV and 8 for fp8: about 100-200 KB per CU; random
-// 256-byte row gathers need that much in flight to approach HBM bandwidth). K rows land in an AGPR ring in
-// MFMA operand layout; V rows go straight to a per-wave LDS ring by DMA
-// (global_load_lds). Slots are looked up 2S-3 tiles ahead of compute. All of these are
+// 256-byte row gathers need that much in flight to approach HBM bandwidth). Every load
+// instruction reads whole rows (1 KB: 64 / (row bytes / 16) rows) with the nontemporal
+// hint. K rows land in an AGPR ring and pass through a one-tile per-wave LDS staging
+// buffer into MFMA operand order when their tile is computed; V rows go straight to a
+// per-wave LDS ring by DMA (global_load_lds). Slots are looked up 2S-3 tiles ahead of compute. All of these are
 // issued as inline assembly and waited for with explicit counts. The issue cursor clamps
 // at the wave's last tile, so the pipelined loop has no data-dependent branches around
 // loads and the counts stay exact.
@@ -300,8 +302,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   static_assert(TB == 2 || !kFp8, "fp8 V^T reads assume 32-key tiles");
   constexpr int kStage = kTile * kRowB;     // bytes of one V tile
   constexpr int kVL = kStage / 1024;        // 16-byte V loads per lane per tile
-  constexpr int KR = kFp8 ? KK / 2 : KK;    // 16-byte K loads per lane per 16-token block
-  constexpr int OPS = 1 + kVL + TB * KR;    // vector memory instructions per pipeline step
+  constexpr int OPS = 1 + 2 * kVL;          // vector memory instructions per pipeline step
   // Pipeline stages: K of S tiles in a register ring, V of S tiles in an LDS ring. Each
   // step issues OPS vector memory instructions (one slot lookup, the V DMA, the K loads);
   // a wave can have at most 63 outstanding, which bounds S: 4 for 16-bit KV at D=128
@@ -314,16 +315,17 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   static_assert(kVL >= 1 && 64 % kCPR == 0, "a V load covers whole rows");
 
   __shared__ __attribute__((aligned(16))) unsigned char vring[kWaves][S][kStage];
+  // K of the tile being computed, staged from the register ring into operand order
+  __shared__ __attribute__((aligned(16))) unsigned char kstage[kWaves][kStage];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
   const int j = lane >> 4;
   const int W = blockIdx.x * kWaves + wave;
-  // Head-dim order of the QK contraction. K load x of a lane (c, j) reads bytes
-  // x*64 + j*16 .. +16 of its token's row, so each load instruction reads 64 contiguous
-  // bytes of 16 rows; MFMA step kk then holds dims qdim(kk) .. +8 of lane group j, and
-  // the query rows are loaded in the same order.
+  // Head-dim order of the QK contraction: MFMA step kk of lane group j holds the K row's
+  // 16-byte chunk 4*kk + j (16-bit KV; fp8: chunk 4*(kk/2) + j, half kk%2), that is
+  // dims qdim(kk) .. +8, and the query rows are loaded in the same order.
   auto qdim = [&](int kk) -> int {
     if constexpr (kFp8) return (kk >> 1) * 64 + j * 16 + (kk & 1) * 8;
     else return kk * 32 + j * 8;
@@ -359,10 +361,18 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     if constexpr (kFp8) return kCPR >= 8 ? ((t & 3) | ((t >> 2) & 4)) : (t & (kCPR - 1));
     else return (2 * t) & (kCPR - 2);
   };
+  // XOR swizzle of the 16-byte chunks of K row t in the staging buffer: the 16 rows an
+  // operand read takes one chunk from land in 16 different 16-byte columns of a 256-byte
+  // bank period (a row of kRowB bytes spans 256 / kRowB rows of a period).
+  auto swzk = [](int t) -> int {
+    constexpr int kRowsPerPeriod = kRowB >= 256 ? 1 : 256 / kRowB;
+    constexpr int kCols = kCPR < 16 ? kCPR : 16;
+    return (t / kRowsPerPeriod) & (kCols - 1);
+  };
 
   // ---- per-tile K register ring (V goes to the LDS ring by DMA) ----
   struct Raw {
-    u32x4 k[TB][KR];
+    u32x4 k[kVL];  // whole K rows: load x holds rows (64 / kCPR) x + lane / kCPR
   };
   Raw ring[S];
   int sreg[S];
@@ -406,15 +416,15 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + x * 1024);
       __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" MA_V_POLICY : : "s"(m0), "v"(src) : "memory", "m0");
     }
+    // K: whole rows per instruction, like V; lane chunk `pos` takes the row's chunk
+    // pos ^ swzk(tok), so that the staging copy below is a linear store
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int slot = shfl_i(myslot, tb * 16 + c);
-      const unsigned char MA_GLOBAL* kp = kbase + (int64_t)slot * row_bytes + hoff;
-#pragma unroll
-      for (int x = 0; x < KR; ++x) {
-        const int off = x * 64 + j * 16;  // 64 contiguous bytes of the row per instruction
-        __asm__ volatile("global_load_dwordx4 %0, %1, off" MA_K_POLICY : "=a"(r.k[tb][x]) : "v"(kp + off) : "memory");
-      }
+    for (int x = 0; x < kVL; ++x) {
+      const int tok = (64 / kCPR) * x + lane / kCPR;
+      const int pos = lane % kCPR;
+      const int slot = shfl_i(myslot, tok);
+      const unsigned char MA_GLOBAL* kp = kbase + (int64_t)slot * row_bytes + hoff + ((pos ^ swzk(tok)) << 4);
+      __asm__ volatile("global_load_dwordx4 %0, %1, off" MA_K_POLICY : "=a"(r.k[x]) : "v"(kp) : "memory");
     }
   };
 
@@ -426,9 +436,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   };
   auto touch_k = [&](Raw& r) __attribute__((always_inline)) {
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-      for (int x = 0; x < KR; ++x) __asm__ volatile("" : "+a"(r.k[tb][x]));
+    for (int x = 0; x < kVL; ++x) __asm__ volatile("" : "+a"(r.k[x]));
   };
 
   // ---- per-segment state ----
@@ -541,16 +549,23 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   auto compute = [&](const Cursor& cu, const Raw& r, int stage) __attribute__((always_inline)) {
     const int tb0 = cu.g.lo_min + cu.tile * kTile;
     const unsigned char* vt = vring[wave][stage];
-    // ---- K operand ----
+    // ---- K operand: the tile's rows through the staging buffer into operand order ----
+    unsigned char* ks = kstage[wave];
+#pragma unroll
+    for (int x = 0; x < kVL; ++x) *reinterpret_cast<u32x4*>(ks + x * 1024 + lane * 16) = r.k[x];
     u32x4 kr[TB][KK];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
+      const int t = tb * 16 + c;
+      auto chunk = [&](int q) -> u32x4 {
+        return *reinterpret_cast<const u32x4*>(ks + t * kRowB + (((4 * q + j) ^ swzk(t)) << 4));
+      };
       if constexpr (kFp8) {
 #pragma unroll
-        for (int half = 0; half < KK / 2; ++half) cvt16_fp8<KV, QBF16>(r.k[tb][half], kr[tb][2 * half], kr[tb][2 * half + 1]);
+        for (int half = 0; half < KK / 2; ++half) cvt16_fp8<KV, QBF16>(chunk(half), kr[tb][2 * half], kr[tb][2 * half + 1]);
       } else {
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) kr[tb][kk] = r.k[tb][kk];
+        for (int kk = 0; kk < KK; ++kk) kr[tb][kk] = chunk(kk);
       }
     }
     // ---- S^T = K Q^T ----
