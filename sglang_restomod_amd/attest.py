@@ -1,17 +1,27 @@
-"""What actually registered, in a form a verifier can read (sglang_restomod/attest.py:1-194).
+"""Attestation record: which components of this plugin registered, for an outside verifier.
 
-Three states per component:
+The record is a JSON object with these keys (the interface the reference's verifier
+reads; format of sglang_restomod/attest.py:138-194):
 
-* loaded (``record(name, True)``): registered and in use;
-* failed (``record(name, False, detail)``): its ``register()`` raised;
-* inactive (``inactive(name, reason)``): loaded cleanly but does nothing; it is
-  also listed as loaded so the two lists stay a partition of "registered".
+``engine``
+    ``{"python": version, "path": module file or null, "version": or null}`` of the
+    ``sglang`` module as imported in this process (null when it is not imported).
+``selected``
+    the component names the environment selected, in order.
+``components``
+    ``{name: {"ok": bool, "detail": text}}``; ``detail`` is present only when there is
+    one. An inactive component's detail starts with ``"registered, inactive: "``.
+``loaded`` / ``failed`` / ``inactive``
+    names by outcome, in the order the outcomes were first reported. ``inactive`` is a
+    subset of ``loaded`` (the component registered without error but serves nothing).
+``missing``
+    selected names with no outcome at all.
 
-``snapshot()`` returns the record plus the imported engine's identity, and
-lists as ``missing`` any selected name with no record. ``write()`` dumps the
-snapshot as JSON to ``SGLANG_RESTOMOD_ATTEST`` (or a given path) through a
-per-call temporary file and an atomic rename, so several ranks writing the same
-target do not trip over one shared temporary name. No function here raises.
+Design: one ``_Outcome`` per component in an insertion-ordered table; the lists are
+derived from it when a snapshot is taken, so they cannot disagree. ``write`` renders
+the snapshot into a uniquely named sibling file and renames it over the target, so
+concurrent writers (one per rank) never share a partial file. Nothing here raises into
+the caller: attestation is an observer and must not stop a launch.
 """
 
 from __future__ import annotations
@@ -19,118 +29,115 @@ from __future__ import annotations
 import json
 import logging
 import os
+import secrets
 import sys
-import tempfile
-from typing import Any
+from dataclasses import dataclass
+from typing import Any, Optional
 
 logger = logging.getLogger(__name__)
 
 ENV_ATTEST = "SGLANG_RESTOMOD_ATTEST"
+INACTIVE_PREFIX = "registered, inactive: "
 
 
-def _empty() -> dict[str, Any]:
-    return {"selected": [], "components": {}, "loaded": [], "failed": [], "inactive": []}
+@dataclass
+class _Outcome:
+    ok: bool
+    detail: str = ""
+    idle: bool = False  # registered, but serves nothing
+
+    def as_json(self) -> dict[str, Any]:
+        out: dict[str, Any] = {"ok": self.ok}
+        if self.detail:
+            out["detail"] = self.detail
+        return out
 
 
-_STATE: dict[str, Any] = _empty()
+class _Ledger:
+    def __init__(self) -> None:
+        self.selected: list[str] = []
+        self.outcomes: dict[str, _Outcome] = {}
+
+    def names(self, pred) -> list[str]:
+        return [name for name, o in self.outcomes.items() if pred(o)]
+
+
+_LEDGER = _Ledger()
 
 
 def reset() -> None:
-    """Forget everything (tests)."""
-    _STATE.clear()
-    _STATE.update(_empty())
+    """Forget every outcome and the selection (tests)."""
+    global _LEDGER
+    _LEDGER = _Ledger()
 
 
 def set_selected(names: list[str]) -> None:
-    _STATE["selected"] = list(names)
-
-
-def engine() -> dict[str, Any]:
-    """The engine as imported (module path and its own ``__version__``), not as installed."""
-    mod = sys.modules.get("sglang")
-    return {
-        "python": sys.version.split()[0],
-        "path": getattr(mod, "__file__", None) if mod is not None else None,
-        "version": getattr(mod, "__version__", None) if mod is not None else None,
-    }
-
-
-def _add(key: str, name: str) -> None:
-    if name not in _STATE[key]:
-        _STATE[key].append(name)
-
-
-def _drop(key: str, name: str) -> None:
-    if name in _STATE[key]:
-        _STATE[key].remove(name)
+    _LEDGER.selected = [str(n) for n in names]
 
 
 def record(name: str, ok: bool, detail: str = "") -> None:
-    """One component's registration outcome; keeps an earlier inactive reason if none is given."""
-    entry: dict[str, Any] = {"ok": bool(ok)}
-    previous = _STATE["components"].get(name) or {}
-    if detail:
-        entry["detail"] = detail
-    elif previous.get("detail"):
-        entry["detail"] = previous["detail"]
-    _STATE["components"][name] = entry
+    """Report one component's registration: ``ok`` True for a clean ``register()``, False
+    for one that raised. A success without a detail keeps what an earlier report said
+    (an inactive reason survives the later success report); a failure ends any inactive
+    state."""
+    prev = _LEDGER.outcomes.get(name)
     if ok:
-        _add("loaded", name)
-        _drop("failed", name)
+        idle = prev.idle if prev is not None else False
+        text = detail or (prev.detail if prev is not None else "")
+        _LEDGER.outcomes[name] = _Outcome(True, text, idle)
     else:
-        _add("failed", name)
+        _LEDGER.outcomes[name] = _Outcome(False, detail, False)
 
 
 def inactive(name: str, reason: Any) -> None:
-    """A component that registered (or was selected) but will do nothing. Never raises."""
+    """Report a component that registered (or was selected) but serves nothing."""
     try:
-        text = str(reason)
-    except Exception:  # noqa: BLE001
-        text = "<unprintable reason>"
-    try:
-        entry = _STATE["components"].setdefault(name, {"ok": True})
-        entry["detail"] = "registered, inactive: " + text
-        _add("inactive", name)
-        _drop("failed", name)
-        _add("loaded", name)
-    except Exception:  # noqa: BLE001
-        logger.debug("attest.inactive(%s) failed", name, exc_info=True)
+        text = f"{reason}"
+    except Exception:  # noqa: BLE001 - a reason that cannot print is still a reason
+        text = "<reason could not be printed>"
+    _LEDGER.outcomes[name] = _Outcome(True, INACTIVE_PREFIX + text, True)
+
+
+def engine() -> dict[str, Any]:
+    """Identity of the engine as this process imported it (not as some installer put it)."""
+    module = sys.modules.get("sglang")
+    return {
+        "python": sys.version.split()[0],
+        "path": None if module is None else getattr(module, "__file__", None),
+        "version": None if module is None else getattr(module, "__version__", None),
+    }
 
 
 def snapshot() -> dict[str, Any]:
-    snap = {
+    led = _LEDGER
+    return {
         "engine": engine(),
-        "selected": list(_STATE["selected"]),
-        "loaded": list(_STATE["loaded"]),
-        "failed": list(_STATE["failed"]),
-        "inactive": list(_STATE["inactive"]),
-        "components": {k: dict(v) for k, v in _STATE["components"].items()},
+        "selected": list(led.selected),
+        "components": {name: o.as_json() for name, o in led.outcomes.items()},
+        "loaded": led.names(lambda o: o.ok),
+        "failed": led.names(lambda o: not o.ok),
+        "inactive": led.names(lambda o: o.idle),
+        "missing": [n for n in led.selected if n not in led.outcomes],
     }
-    snap["missing"] = [n for n in snap["selected"] if n not in snap["components"]]
-    return snap
 
 
-def write(path: str | None = None) -> str | None:
-    """Write the snapshot as JSON; return the path written or None (unset or unwritable)."""
-    target = path or os.environ.get(ENV_ATTEST)
+def write(path: Optional[str] = None) -> Optional[str]:
+    """Write the snapshot to ``path`` (default: ``$SGLANG_RESTOMOD_ATTEST``). Returns the
+    path written, or None when no target is set or the write failed."""
+    target = path if path else os.environ.get(ENV_ATTEST, "")
     if not target:
         return None
-    tmp = None
+    staging = f"{target}.{os.getpid()}.{secrets.token_hex(4)}.part"
     try:
-        payload = snapshot()
-        folder = os.path.dirname(target) or "."
-        fd, tmp = tempfile.mkstemp(dir=folder, prefix=os.path.basename(target) + ".", suffix=".tmp")
-        with os.fdopen(fd, "w", encoding="utf-8") as fh:
-            json.dump(payload, fh, indent=1, sort_keys=True)
-            fh.write("\n")
-        os.replace(tmp, target)
-        tmp = None
-    except Exception:  # noqa: BLE001 - an observer's file never stops a launch
-        logger.warning("could not write attestation to %s", target, exc_info=True)
-        if tmp is not None:
-            try:
-                os.remove(tmp)
-            except OSError:
-                pass
+        text = json.dumps(snapshot(), indent=2, sort_keys=True) + "\n"
+        with open(staging, "x", encoding="utf-8") as fh:  # "x": never reuse another writer's file
+            fh.write(text)
+        os.replace(staging, target)
+        return target
+    except Exception:  # noqa: BLE001 - report, never raise into the engine's startup
+        logger.warning("attestation not written to %s", target, exc_info=True)
+        try:
+            os.unlink(staging)
+        except OSError:
+            pass
         return None
-    return target
