@@ -151,9 +151,9 @@ def _runner(w):
             max_q_per_seq=T, softmax_scale=w.softmax_scale, out=out, row_index=w.req_pool_indices,
             max_seq_len_hint=hint)
     return lambda: ops.paged_forward(
-        w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens, out=out,
+        w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens, out=out, block_size=1,
         softmax_scale=w.softmax_scale, causal=True, row_index=w.req_pool_indices,
-        max_seq_len_hint=hint, max_q_len_hint=T)
+        max_seq_len_hint=hint, max_q_len_hint=T)[0]
 
 
 WARMUP_MIN_S = 0.5

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 7
+#define MA_ABI_VERSION 8
 
 /* dtype codes */
 #define MA_DT_F16 0
@@ -113,7 +113,10 @@ int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
  * (_paged_adapter.py:613-660) and its kernels (_kernels_paged_verify.py:52-433).
  *   q [num_tokens, num_q_heads, head_dim]; query_start_loc [batch+1];
  *   prefix_lens [batch] (NULL: seq_lens - query count); seq_lens [batch] total keys;
- *   max_q_per_seq: upper bound of query tokens per sequence (<= 64)
+ *   max_q_per_seq: the longest chain expected (1..64); it picks the row-group shape
+ *     (16 or 32 rows). A sequence with more query tokens is still computed in full.
+ *   Query rows are clamped into [0, num_tokens): metadata pointing outside q / out
+ *     shortens a sequence instead of addressing memory past the buffers.
  *   num_workgroups / workspace: as for ma_grouped_decode
  */
 int ma_paged_verify(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
@@ -146,6 +149,7 @@ size_t ma_extend_workspace_bytes(int64_t num_tokens, int num_q_heads, int num_kv
  * j >= prefix_lens[b] + i - window when sliding_window >= 0 (a left bound, also for
  * non-causal layers).
  *   prefix_lens NULL: seq_lens - query count.
+ *   Query rows are clamped into [0, num_tokens), as for ma_paged_verify.
  *   batch <= 16384. No host-side maximum of the query lengths is needed: a plan kernel
  *   lists the row tiles on the device (reference: max_seq_len from seq_lens.max().item(),
  *   _paged_adapter.py:605-606).
@@ -197,6 +201,28 @@ int ma_set_kv_buffer(const void* k, const void* v, int64_t src_stride_tok, int64
 int ma_translate_slots(const int32_t* table, int64_t table_stride, const int64_t* row_index,
                        const int32_t* seq_lens, int batch, const int64_t* mapping, int64_t mapping_len,
                        int32_t* out, int64_t out_stride, int width, void* stream);
+
+/*
+ * Key rows of a multi-step speculative draft, on the device.
+ * Replaces the per-step draft KV-index build of the reference's draft container
+ * (draft_decode.py:172-208, the engine container's common_template)
+ * and its per-step page-table conversion (draft_decode_plan.py:42-78). Row
+ * r = b * topk + k of out is branch k of request b:
+ *   out[r * out_stride + j] = T(b, j)                      for j < seq_lens[b]
+ *   out[r * out_stride + j] = T(b, j + k * num_steps)      for seq_lens[b] <= j < seq_lens[b] + num_steps
+ *   T(b, p) = table[row * table_stride + p] (0 when p >= table_width), row = row_index ?
+ *   row_index[b] : b, passed through mapping (int64 [mapping_len], a slot outside gives 0)
+ *   when mapping is not NULL.
+ * This is the engine's placement of draft tokens in req_to_token (branch k's num_steps
+ * tokens follow the prefix at k * num_steps) for page size 1, or for any page size with
+ * topk 1. Draft step i then attends over the first seq_lens[b] + i + 1 entries of each
+ * row (ma_grouped_decode with table = out, row_index NULL). Entries from
+ * min(seq_lens[b] + num_steps, width) on are not written.
+ * batch * topk <= 65535; out_stride >= width; table_stride >= table_width.
+ */
+int ma_draft_table(const int32_t* table, int64_t table_stride, int table_width, const int64_t* row_index,
+                   const int32_t* seq_lens, int batch, int topk, int num_steps, const int64_t* mapping,
+                   int64_t mapping_len, int32_t* out, int64_t out_stride, int width, void* stream);
 
 /*
  * fp8 paged KV decoded into fp16 logical pages.

@@ -16,6 +16,17 @@
   verify ("smallq") views: every query row repeats its sequence's page table
   and sees ``prefix + i + 1`` keys (:514-545).
   Pinned by hand-computed vectors in ``tests/test_oracle_metadata.py``.
+* ``draft_rows`` restates the key rows of a multi-step draft round: row
+  ``b * topk + k`` is request ``b``'s prefix ``req_to_token[req, :seq_b]`` followed by
+  branch ``k``'s ``num_steps`` draft slots at ``req_to_token[req, seq_b + k * num_steps + s]``.
+  The rule is the engine's placement of draft tokens at page size 1 (or top-k 1), which
+  the reference's draft container consumes through the engine's per-step index builder
+  (sglang_restomod/attention/v100/draft_decode.py:172-208; the builder itself is
+  upstream SGLang 0.5.23, not in the reference). Pinned by the closed form at top-k 1
+  (each row is the request's own ``req_to_token`` row), by the invariant that the
+  branches' draft regions tile ``[seq_b, seq_b + topk * num_steps)`` without overlap,
+  and by hand-computed vectors (``tests/test_oracle_metadata.py``). Against the engine's
+  own builder it is parity unpinned (no vector of it exists in the reference).
 """
 
 from __future__ import annotations
@@ -76,3 +87,24 @@ def build_extend_metadata(req_to_token: Sequence[Sequence[int]], req_pool_indice
         md["smallq_page_table"] = sq_table
         md["smallq_seq_lens"] = sq_seq
     return md
+
+
+def draft_rows(req_to_token: Sequence[Sequence[int]], req_pool_indices: Sequence[int], seq_lens: Sequence[int],
+               topk: int, num_steps: int, mapping: Sequence[int] | None = None) -> List[List[int]]:
+    """Rows ``b * topk + k``: prefix slots, then branch ``k``'s ``num_steps`` draft slots
+    (positions past the table's width read as slot 0; ``mapping`` translates every slot,
+    one outside it giving 0)."""
+    def at(row, p):
+        slot = int(row[p]) if p < len(row) else 0
+        if mapping is not None:
+            slot = int(mapping[slot]) if 0 <= slot < len(mapping) else 0
+        return slot
+
+    out = []
+    for b, seq in enumerate(seq_lens):
+        row = req_to_token[int(req_pool_indices[b])]
+        seq = max(int(seq), 0)
+        for k in range(topk):
+            out.append([at(row, j) for j in range(seq)] +
+                       [at(row, seq + k * num_steps + s) for s in range(num_steps)])
+    return out

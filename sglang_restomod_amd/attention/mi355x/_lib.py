@@ -61,6 +61,12 @@ SIGNATURES = {
         c_void_p, c_int64,                            # mapping, mapping_len
         c_void_p, c_int64, c_int, c_void_p,           # out, stride, width, stream
     ]),
+    "ma_draft_table": (c_int, [
+        c_void_p, c_int64, c_int, c_void_p,           # table, stride, width, row_index
+        c_void_p, c_int, c_int, c_int,                # seq_lens, batch, topk, num_steps
+        c_void_p, c_int64,                            # mapping, mapping_len
+        c_void_p, c_int64, c_int, c_void_p,           # out, stride, width, stream
+    ]),
     "ma_gather_fp8_paged_kv": (c_int, [
         c_void_p, c_void_p, c_int64, c_int64, c_int64,  # caches, page/token/head strides (bytes)
         c_int, c_int64, c_void_p, c_int64, c_void_p,  # dtype, num_pages, page_table, stride, seq_lens

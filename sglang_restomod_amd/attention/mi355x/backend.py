@@ -20,8 +20,8 @@ What differs by design:
   and nothing synchronises with the host (the reference reads
   ``seq_lens.max().item()`` here, :457). The extend kernel lists its row tiles on
   the device, and the sliding-window table of an SWA pool is translated on the
-  device row by row (``ops.translate_slots``). Only a draft extend without
-  ``extend_seq_lens_cpu`` reads its longest chain from the device, to route it.
+  device row by row (``ops.translate_slots``). Routing a draft extend to the verify
+  kernel uses host-known shapes only (token and request counts), never device values.
 * fp8 KV (e4m3fn / e5m2, per-tensor scale) is read directly by every kernel; the
   reference's fp16 prefill scratch (:277-330, gather at :1226-1253) is not needed.
 """
@@ -50,8 +50,8 @@ FP8_KV = (torch.float8_e4m3fn, torch.float8_e5m2)
 MODE_DECODE = "decode"
 MODE_EXTEND = "extend"
 MODE_VERIFY = "verify"
-# write new K/V with this library's kernel into the pool's buffers instead of calling the
-# pool's own set_kv_buffer (same stored bytes; see ops.set_kv_buffer)
+# new K/V go into the pool's buffers through this library's kernel (ops.set_kv_buffer: the
+# same stored bytes as the pool's own set_kv_buffer); "0" calls the pool's method instead
 ENV_NATIVE_KV_WRITE = "SGLANG_MI355X_NATIVE_KV_WRITE"
 
 
@@ -116,7 +116,7 @@ class MI355XAttnBackend(_EngineBase):
         if self.req_to_token.dtype != torch.int32:
             raise ValueError("req_to_token must be int32")
         self.head_dim = head_dim
-        self.native_kv_write = env_flag(ENV_NATIVE_KV_WRITE, "0")
+        self.native_kv_write = env_flag(ENV_NATIVE_KV_WRITE, "1")
         self.forward_metadata: Optional[MI355XForwardMetadata] = None
         self._workspace: Optional[torch.Tensor] = None
         self._extend_ws: Optional[torch.Tensor] = None
@@ -215,17 +215,20 @@ class MI355XAttnBackend(_EngineBase):
             return
         ext_cpu = getattr(forward_batch, "extend_seq_lens_cpu", None)
         max_q = int(max(ext_cpu)) if ext_cpu is not None and len(ext_cpu) else None
-        # a draft extend is a few rows over the whole prefix: the verify kernel's shape
-        draft = _mode_is(mode, "is_draft_extend_v2") or _mode_is(mode, "is_draft_extend")
-        if draft and max_q is None and forward_batch.extend_seq_lens.numel():
-            # routing needs the longest chain (the reference reads it the same way)
-            max_q = int(forward_batch.extend_seq_lens.max().item())
         md = self.build_metadata(
             MODE_EXTEND, forward_batch.req_pool_indices, forward_batch.seq_lens,
             forward_batch.extend_seq_lens, forward_batch.extend_prefix_lens,
             max_q_per_seq=max_q, seq_lens_cpu=seq_lens_cpu)
-        if draft and 0 < md.max_q_per_seq <= ops.VERIFY_MAX_Q_PER_SEQ:
+        # a draft extend is a few rows per request over the whole prefix, the verify kernel's
+        # shape. Routed by host-known sizes (the reference reads the longest chain with
+        # .item() instead, _paged_adapter.py:613-617): at most VERIFY_MAX_Q_PER_SEQ rows per
+        # request on average; the longest chain, when the host has it, picks the row groups.
+        draft = _mode_is(mode, "is_draft_extend_v2") or _mode_is(mode, "is_draft_extend")
+        batch = int(forward_batch.req_pool_indices.shape[0])
+        tokens = int(forward_batch.out_cache_loc.shape[0])
+        if draft and batch and tokens <= batch * ops.VERIFY_MAX_Q_PER_SEQ:
             md.mode = MODE_VERIFY
+            md.max_q_per_seq = max(1, min(max_q if max_q else tokens, ops.VERIFY_MAX_Q_PER_SEQ))
         self.forward_metadata = md
 
     # ------------------------------------------------------------------
@@ -296,6 +299,13 @@ class MI355XAttnBackend(_EngineBase):
             self._cg_query_start_loc[: bs + 1].copy_(
                 torch.arange(0, (bs + 1) * n, n, dtype=torch.int32, device=seq.device))
             mode, max_q = MODE_VERIFY, n
+        elif _mode_is(forward_mode, "is_draft_extend_v2") or _mode_is(forward_mode, "is_draft_extend"):
+            # the graph API carries neither the prefix nor the rows of each request, and the
+            # engine's per-request row counts in a captured draft extend are not pinned here
+            # (the reference hands these graphs to another backend, :747, :801)
+            raise NotImplementedError(
+                "mi355x_attn does not capture draft-extend graphs (per-request rows are not part of the "
+                "capture/replay arguments); run the draft extend eagerly")
         else:
             # captured extend: the tokens of each sequence are all new (the reference
             # approximates the same way, :838-843); the grid covers num_tokens rows
@@ -375,7 +385,9 @@ class MI355XAttnBackend(_EngineBase):
     def _save_kv(self, layer, loc, k, v) -> None:
         if k is None:
             return
-        if not self.native_kv_write:
+        # an SWA pool maps full-pool slots to its own for its sliding-window layers inside
+        # its set_kv_buffer; the native write is for pools that store at the slots given
+        if not self.native_kv_write or self._has_swa_pool():
             self.token_to_kv_pool.set_kv_buffer(layer, loc, k, v, layer.k_scale, layer.v_scale)
             return
         k_cache, v_cache = self._caches(layer)
@@ -429,7 +441,7 @@ class MI355XAttnBackend(_EngineBase):
         if q3.shape[0]:
             table, rows = self._table_for(md, window)
             ks, vs = self._scales(layer)
-            ops.paged_forward(
+            ops.paged_forward(  # returns (out, softmax_lse); out is written in place
                 q3, k_cache, v_cache, table, md.seq_lens, md.query_start_loc, md.prefix_kv_lens,
                 out=out, block_size=1, num_kv_heads=int(layer.tp_k_head_num),
                 softmax_scale=float(layer.scaling), causal=causal, sliding_window_size=window,

@@ -1,83 +1,108 @@
-"""Let a draft worker name this backend (the contract of
+"""Let a draft worker select this backend (the role of
 sglang_restomod/attention/v100/draft_backend.py:31-83).
 
-The engine builds a draft worker's attention backends from a fixed name map in its
-``DraftBackendFactory``. ``install_on`` patches the factory so that
-``--speculative-draft-attention-backend mi355x_attn`` resolves:
+The engine builds a draft worker's attention from a fixed name table in its
+``DraftBackendFactory``. ``install_on`` reroutes two of the factory's methods by the
+selected name: when it is one of ``NAMES``,
 
-* draft **extend** gets ``MI355XAttnBackend`` (wrapped by the engine's draft-extend
-  wrapper): a few rows per request over the whole prefix, which the backend serves
-  with the split-KV verify kernel;
-* draft **decode** (more than one speculative step) gets the split-KV multi-step
-  container of ``draft_decode``, or the engine's Triton container when
-  ``draft_decode.unsupported_reason`` names a reason.
+* ``create_draft_extend_backend`` returns ``MI355XAttnBackend`` inside the engine's
+  draft-extend wrapper (a draft extend is a few rows per request over the whole
+  prefix, which the backend serves with its split-KV verify kernel);
+* ``create_decode_backend`` returns the split-KV multi-step container of
+  ``draft_decode`` for drafts of two or more steps. A draft worker it cannot serve
+  raises ``NotImplementedError`` from the container; nothing is handed to another
+  backend.
 
-The hooks are injected so the patch is testable without the engine; patching twice
-changes nothing.
+Every other name reaches the engine's own methods unchanged. The engine pieces are
+injected, so the routing is testable without the engine. The factory keeps the
+original methods, so a second ``install_on`` is a no-op and ``uninstall`` restores them.
 """
 
 from __future__ import annotations
 
 import logging
+from typing import Callable, Optional
 
 from .backend_registry import MI355X_ATTN, V100_ALIAS
 
 logger = logging.getLogger(__name__)
 
-FLAG = "_restomod_mi355x_draft"
-DRAFT_DECODE_FALLBACK = "triton"
 NAMES = (MI355X_ATTN, V100_ALIAS)
+_SAVED = "_mi355x_attn_saved_methods"
+_ROUTED = ("create_draft_extend_backend", "create_decode_backend")
 
 
-def install_on(factory, build, wrap, build_native=None, names=NAMES) -> bool:
-    """Patch ``factory`` (the engine's DraftBackendFactory class); True if anything changed.
+class _Routes:
+    """What the two rerouted methods do for our names."""
 
-    ``build(runner)`` returns the backend, ``wrap(runner, backend)`` is the engine's
-    draft-extend wrapper, ``build_native(runner, topk, steps, stamp)`` returns the
-    split-KV draft-decode container or None.
-    """
-    if getattr(factory, FLAG, False):
-        return False
-    original_extend = factory.create_draft_extend_backend
-    original_decode = factory.create_decode_backend
+    def __init__(self, build: Callable, wrap: Callable, build_container: Optional[Callable]):
+        self.build = build
+        self.wrap = wrap
+        self.build_container = build_container
 
-    def create_draft_extend_backend(self):
-        if self.draft_attn_backend not in names:
-            return original_extend(self)
-        backend = build(self.draft_model_runner)
-        if backend is None:
-            return None
-        wrapped = wrap(self.draft_model_runner, backend)
+    def create_draft_extend_backend(self, factory):
+        runner = factory.draft_model_runner
+        backend = self.build(runner)
+        wrapped = None if backend is None else self.wrap(runner, backend)
         if wrapped is not None:
-            wrapped.prefill_attention_backend_str = self.draft_attn_backend
-            wrapped.decode_attention_backend_str = self.draft_attn_backend
+            for attr in ("prefill_attention_backend_str", "decode_attention_backend_str"):
+                setattr(wrapped, attr, factory.draft_attn_backend)
         return wrapped
 
-    def create_decode_backend(self):
-        if self.draft_attn_backend not in names:
-            return original_decode(self)
-        if self.speculative_num_steps > 1:
-            builder = build_native
-            if builder is None:
-                from .draft_decode import build_native as builder
-            native = builder(self.draft_model_runner, self.topk, self.speculative_num_steps, self.draft_attn_backend)
-            if native is not None:
-                return native
-        saved = self.draft_attn_backend
-        self.draft_attn_backend = DRAFT_DECODE_FALLBACK
-        try:
-            return original_decode(self)
-        finally:
-            self.draft_attn_backend = saved
+    def create_decode_backend(self, factory, engine_method):
+        if int(factory.speculative_num_steps) < 2:
+            # a one-step draft has no decode passes: whatever the engine returns for it
+            return engine_method(factory)
+        make = self.build_container
+        if make is None:
+            from .draft_decode import build_native as make
+        return make(factory.draft_model_runner, int(factory.topk), int(factory.speculative_num_steps),
+                    factory.draft_attn_backend)
 
-    factory.create_draft_extend_backend = create_draft_extend_backend
-    factory.create_decode_backend = create_decode_backend
-    setattr(factory, FLAG, True)
+
+def install_on(factory, build, wrap, build_container=None, names=NAMES) -> bool:
+    """Reroute ``factory`` (the engine's DraftBackendFactory class) for ``names``; True if
+    it was not rerouted before.
+
+    ``build(runner)`` makes the backend, ``wrap(runner, backend)`` is the engine's
+    draft-extend wrapper, ``build_container(runner, topk, steps, name)`` makes the
+    multi-step decode container (default: ``draft_decode.build_native``).
+    """
+    if _SAVED in vars(factory):
+        return False
+    saved = {name: getattr(factory, name) for name in _ROUTED}
+    routes = _Routes(build, wrap, build_container)
+    ours = frozenset(names)
+
+    def draft_extend(self):
+        if self.draft_attn_backend in ours:
+            return routes.create_draft_extend_backend(self)
+        return saved["create_draft_extend_backend"](self)
+
+    def decode(self):
+        if self.draft_attn_backend in ours:
+            return routes.create_decode_backend(self, saved["create_decode_backend"])
+        return saved["create_decode_backend"](self)
+
+    setattr(factory, _SAVED, saved)
+    factory.create_draft_extend_backend = draft_extend
+    factory.create_decode_backend = decode
+    return True
+
+
+def uninstall(factory) -> bool:
+    """Give ``factory`` its own methods back; True if it was rerouted."""
+    saved = vars(factory).get(_SAVED)
+    if saved is None:
+        return False
+    for name, method in saved.items():
+        setattr(factory, name, method)
+    delattr(factory, _SAVED)
     return True
 
 
 def install() -> bool:
-    """Component hook: patch the engine's draft factory when the engine is importable."""
+    """Component hook: reroute the engine's draft factory when the engine is importable."""
     try:
         from sglang.srt.layers.attention.attention_registry import attn_backend_wrapper_for_draft_extend
         from sglang.srt.speculative import draft_utils

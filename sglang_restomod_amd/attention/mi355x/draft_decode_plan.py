@@ -1,32 +1,18 @@
 """Planning helpers for draft decode (sglang_restomod/attention/v100/draft_decode_plan.py:42-104).
 
-A multi-step draft container hands each step a flat ``kv_indptr`` /
-``kv_indices`` pair. ``page_table_from_indices`` turns that into the page table
-plus per-row visible length the split-KV decoder takes, entirely on device (no
-host synchronisation, so it is safe inside a captured graph).
-``layer_shape_reason`` says why the decoder cannot serve a layer, or None.
+``page_table_from_indices`` turns a flat ``kv_indptr`` / ``kv_indices`` list into the page
+table plus per-row visible length of a page-granular decoder, entirely on device (no host
+synchronisation, so it is safe inside a captured graph); the split-KV decoder here reads
+such a list in place (``draft_decode.DraftRows.from_flat_lists``), and this conversion
+serves callers that hold page tables. ``layer_shape_reason`` says why the decoder cannot
+serve a layer, or None.
 """
 
 from __future__ import annotations
 
-import os
-from collections.abc import Mapping
-
 import torch
 
-from .backend_registry import env_flag
-
-ENV_FLAG = "SGLANG_MI355X_DRAFT_DECODE_NATIVE"
-PAGE_SIZE = 1
 SUPPORTED_HEAD_DIMS = (64, 128, 256)  # the kernels' head dims (ops.SUPPORTED_HEAD_DIMS)
-
-
-def native_enabled(env: Mapping[str, str] | None = None) -> bool:
-    source = os.environ if env is None else env
-    value = source.get(ENV_FLAG)
-    if value is None or not value.strip():
-        return True
-    return env_flag(ENV_FLAG, "1", source)
 
 
 def page_table_from_indices(
@@ -34,7 +20,7 @@ def page_table_from_indices(
     kv_indices: torch.Tensor,
     page_table: torch.Tensor,
     seq_lens: torch.Tensor,
-    page_size: int = PAGE_SIZE,
+    page_size: int = 1,
 ) -> int:
     """Fill ``page_table[:rows]`` and ``seq_lens[:rows]``; return rows written (0 if the buffers are short).
 

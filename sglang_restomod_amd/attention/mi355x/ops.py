@@ -5,6 +5,7 @@
 * ``set_kv_buffer``          - the token pool's write called at flash_attn_v100_backend.py:1174-1182
 * ``gather_fp8_paged_kv``    - _paged_adapter.py:527-564
 * ``translate_slots``        - the SWA page-table build, flash_attn_v100_backend.py:460-503
+* ``draft_table``            - the draft container's per-step KV rows, draft_decode.py:172-208
 
 Shapes and dtypes are validated here and raise ``ValueError`` the way the
 reference's gates do (_paged_adapter.py:417-418, 538-541). Workspaces are
@@ -266,7 +267,10 @@ def paged_verify_forward(
     num_workgroups: Optional[int] = None,
     workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Few query rows per sequence over a long prefix (linear-chain target verify)."""
+    """Few query rows per sequence over a long prefix (linear-chain target verify).
+
+    ``max_q_per_seq`` is the longest chain expected: it picks the kernel's row-group
+    shape. Every query row of every sequence is computed whatever the hint says."""
     if q.dim() != 3:
         raise ValueError(f"q must be [tokens, heads, head_dim], got {tuple(q.shape)}")
     if v_cache.dtype != k_cache.dtype:
@@ -274,16 +278,20 @@ def paged_verify_forward(
     dev = _check_device(q, k_cache, v_cache, block_table, seq_lens, query_start_loc)
     T, Hq, D = q.shape
     row, head, ps, Hkv, Dk = kv_layout(k_cache, page_size)
+    if kv_layout(v_cache, ps)[:2] != (row, head):
+        raise ValueError("K and V caches must share one layout")
     if Dk != D or Hq % Hkv:
         raise ValueError("head shape mismatch between q and the KV cache")
     if not 0 < max_q_per_seq <= VERIFY_MAX_Q_PER_SEQ:
-        raise ValueError(f"verify serves 1..{VERIFY_MAX_Q_PER_SEQ} query rows per sequence")
+        raise ValueError(f"the verify hint must be 1..{VERIFY_MAX_Q_PER_SEQ} query rows per sequence")
     if q.stride(-1) != 1:
         q = q.contiguous()
     table = _table(block_table)
     B = seq_lens.shape[0]
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
     seq = _i32(seq_lens)
     qsl = _i32(query_start_loc)
     pre = None if prefix_kv_lens is None else _i32(prefix_kv_lens)
@@ -315,7 +323,7 @@ def paged_forward(
     query_start_loc: torch.Tensor,
     prefix_kv_lens: torch.Tensor,
     out: Optional[torch.Tensor] = None,
-    block_size: Optional[int] = None,
+    block_size: Optional[int] = 16,
     num_kv_heads: Optional[int] = None,
     softmax_scale: Optional[float] = None,
     causal: bool = True,
@@ -329,38 +337,48 @@ def paged_forward(
     max_q_len_hint: Optional[int] = None,
     workspace: Optional[torch.Tensor] = None,
 ):
-    """Prefix-aware paged attention over ``q`` [num_tokens, Hq, D] (reference: paged_forward).
+    """Prefix-aware paged attention over ``q`` [num_tokens, Hq, D] (reference: paged_forward,
+    _paged_adapter.py:567-759, same positional arguments). Returns ``(out, softmax_lse)``
+    as the reference does (:756-759); ``softmax_lse`` is an fp32 ``[Hq, num_tokens]``
+    buffer that, as in the reference, is allocated and not filled.
 
-    ``linear_verify`` routes few-row-per-sequence batches to the split-KV verifier
-    (the reference does the same, _paged_adapter.py:613-660). Returns ``out``.
-    ``logical_dense_kv`` is accepted for signature compatibility; it changes no
-    result.
+    ``block_size`` is the page size of ``block_table`` (default 16, the reference's): a
+    4-D cache ``[pages, page_size, Hkv, D]`` must agree with it; a flat pool
+    ``[slots, Hkv, D]`` is read as pages of ``block_size`` rows (``block_size=1`` with
+    ``req_to_token`` / ``row_index`` addresses SGLang's token pool directly).
+    ``linear_verify`` sends batches with at most ``VERIFY_MAX_Q_PER_SEQ`` query rows per
+    sequence on average (a bound from the shapes alone, as the reference routes,
+    :613-617) to the split-KV verifier; ``max_q_len_hint`` (the longest chain) only
+    picks its row-group shape. No host value of the device tensors is read.
+    ``logical_dense_kv`` is accepted for signature compatibility; it changes no result.
     """
     del logical_dense_kv
     T, Hq, D = q.shape
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
+    if block_size is not None and k_cache.dim() == 4 and int(block_size) != k_cache.shape[1]:
+        raise ValueError(f"block_size {block_size} does not match the cache's page dim {k_cache.shape[1]}")
     if num_kv_heads is not None:
         hkv = kv_layout(k_cache, block_size)[3]
         if hkv != int(num_kv_heads):
             raise ValueError(f"num_kv_heads {num_kv_heads} does not match the cache ({hkv})")
     B = seq_lens.shape[0]
-    if linear_verify:
-        if max_q_len_hint is None:
-            # the verifier's grid needs the longest chain (the reference reads the same
-            # bound from the host, _paged_adapter.py:613-617)
-            max_q_len_hint = int((query_start_loc[1:] - query_start_loc[:-1]).max().item()) if B else 0
-        if 0 < max_q_len_hint <= VERIFY_MAX_Q_PER_SEQ:
-            return paged_verify_forward(
-                q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
-                max_q_per_seq=max_q_len_hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
-                causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
-                page_size=block_size, max_seq_len_hint=max_seq_len_hint, workspace=workspace)
-    return paged_extend_forward(
+    lse = torch.empty(Hq, T, dtype=torch.float32, device=q.device)
+    if linear_verify and B > 0 and T <= B * VERIFY_MAX_Q_PER_SEQ:
+        hint = int(max_q_len_hint) if max_q_len_hint else min(T, VERIFY_MAX_Q_PER_SEQ)
+        hint = max(1, min(hint, VERIFY_MAX_Q_PER_SEQ))
+        out = paged_verify_forward(
+            q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
+            max_q_per_seq=hint, softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
+            causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
+            page_size=block_size, max_seq_len_hint=max_seq_len_hint, workspace=workspace)
+        return out, lse
+    out = paged_extend_forward(
         q, k_cache, v_cache, block_table, seq_lens, query_start_loc, prefix_kv_lens,
         softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
         causal=causal, sliding_window_size=sliding_window_size, out=out, row_index=row_index,
         page_size=block_size, workspace=workspace)
+    return out, lse
 
 
 def paged_extend_forward(
@@ -508,6 +526,47 @@ def translate_slots(
         table.data_ptr(), table.stride(0), _ptr(ridx), seq.data_ptr(), B, m64.data_ptr(), m64.numel(),
         out.data_ptr(), out.stride(0), width, _stream_ptr(dev))
     _lib.check(status, "ma_translate_slots")
+    return out
+
+
+def draft_table(
+    table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    topk: int,
+    num_steps: int,
+    row_index: Optional[torch.Tensor] = None,
+    mapping: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    width: Optional[int] = None,
+) -> torch.Tensor:
+    """Key rows of a multi-step draft (``ma_draft_table``): row ``b * topk + k`` holds the
+    prefix slots of request ``b`` (``table[row_index[b], :seq_lens[b]]``) followed by
+    branch ``k``'s ``num_steps`` draft slots, which sit at ``seq_lens[b] + k * num_steps``
+    of the request's row. ``mapping`` (an SWA pool's full-to-SWA index) translates every
+    slot. ``out`` defaults to a new ``[B * topk, width]`` int32 tensor (``width``: the
+    table's); entries past each row's ``seq_lens[b] + num_steps`` are left as they are."""
+    if table.dtype != torch.int32 or table.dim() != 2 or table.stride(1) != 1:
+        raise ValueError("table must be a 2-D int32 tensor with contiguous rows")
+    if topk <= 0 or num_steps <= 0:
+        raise ValueError(f"topk ({topk}) and num_steps ({num_steps}) must be positive")
+    dev = _check_device(table, seq_lens, row_index, mapping)
+    B = int(seq_lens.shape[0])
+    rows = B * int(topk)
+    width = int(table.shape[1] if width is None else width)
+    if out is None:
+        out = torch.empty(rows, width, dtype=torch.int32, device=dev)
+    if out.dtype != torch.int32 or out.dim() != 2 or out.stride(1) != 1 or out.shape[0] < rows or out.shape[1] < width:
+        raise ValueError(f"out must be an int32 [>= {rows}, >= {width}] tensor with contiguous rows")
+    seq = _i32(seq_lens)
+    ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
+    m64 = None
+    if mapping is not None:
+        m64 = mapping if (mapping.dtype == torch.int64 and mapping.is_contiguous()) else mapping.to(torch.int64).contiguous()
+    status = _lib.load().ma_draft_table(
+        table.data_ptr(), table.stride(0), int(table.shape[1]), _ptr(ridx), seq.data_ptr(), B, int(topk),
+        int(num_steps), _ptr(m64), 0 if m64 is None else m64.numel(), out.data_ptr(), out.stride(0), width,
+        _stream_ptr(dev))
+    _lib.check(status, "ma_draft_table")
     return out
 
 

@@ -83,6 +83,7 @@ struct ExtendArgs {
   const int32_t* seq_lens;
   const int32_t* qsl;
   const int32_t* prefix;
+  int num_tokens;        // rows of q and out: query rows are clamped into [0, num_tokens)
   int batch, hq, hkv, group;
   const int64_t* items;  // work list (row_tile_item)
   int causal, window;
@@ -116,6 +117,7 @@ struct ExtendPlanArgs {
   const int32_t* qsl;
   const int32_t* seq_lens;
   const int32_t* prefix;
+  int num_tokens;
   int batch, group, causal, window;
   int tile_rows, tile_keys;  // the extend kernel's rows per workgroup and keys per tile
   int capacity;              // entries of items
@@ -169,7 +171,9 @@ __global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const Exte
   int carry = 0;
   for (int base = 0; base < a.batch; base += kPlanThreads) {
     const int b = base + tid;
-    const int n = b < a.batch ? seq_row_tiles(qsl[b + 1] - qsl[b], a.group, a.tile_rows) : 0;
+    const int n = b < a.batch ? seq_row_tiles(clamp_query_rows(qsl[b], qsl[b + 1], a.num_tokens).ntok, a.group,
+                                              a.tile_rows)
+                              : 0;
     int total;
     const int off = block_exclusive_scan(n, sums, &total);
     if (b < a.batch) start[b] = carry + off;
@@ -189,7 +193,7 @@ __global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const Exte
     }
     const int b = lo;
     const int rt = t - start[b];
-    const int ntok = qsl[b + 1] - qsl[b];
+    const int ntok = clamp_query_rows(qsl[b], qsl[b + 1], a.num_tokens).ntok;
     const int seq = seq_lens[b];
     const int prefix = a.prefix ? gptr(a.prefix)[b] : seq - ntok;
     const KeyRange k = row_tile_keys(rt * a.tile_rows, a.tile_rows, ntok, a.group, prefix, seq, a.causal, a.window);
@@ -289,8 +293,9 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   const int b = (int)(uint32_t)work;
   if (b < 0) return;
   const int rt = (int)(work >> 32);
-  const int tok0 = cptr(a.qsl)[b];
-  const int ntok = cptr(a.qsl)[b + 1] - tok0;
+  const QueryRows qr = clamp_query_rows(cptr(a.qsl)[b], cptr(a.qsl)[b + 1], a.num_tokens);
+  const int tok0 = qr.tok0;
+  const int ntok = qr.ntok;
   const int r0 = rt * kXBM;
   if (r0 >= ntok * a.group) return;
   const int seq = cptr(a.seq_lens)[b];
@@ -696,7 +701,7 @@ extern "C" int ma_paged_extend(
     return set_error(MA_EINVAL, "bad head counts hq=%d hkv=%d", num_q_heads, num_kv_heads);
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
   if (!(softmax_scale * k_scale > 0.f)) return set_error(MA_EINVAL, "softmax scale must be positive");
-  if (num_tokens < 0) return set_error(MA_EINVAL, "num_tokens must be >= 0");
+  if (num_tokens < 0 || num_tokens > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens %lld out of range", (long long)num_tokens);
   if (batch > kPlanMaxBatch) return set_error(MA_EUNSUPPORTED, "batch %d exceeds %d sequences", batch, kPlanMaxBatch);
   if (batch == 0 || num_tokens == 0) return MA_OK;
   if (!q || !k_cache || !v_cache || !table || !seq_lens || !query_start_loc || !out)
@@ -719,6 +724,7 @@ extern "C" int ma_paged_extend(
   if (reinterpret_cast<uintptr_t>(workspace) & 255) return set_error(MA_EINVAL, "workspace must be 256-byte aligned");
   ExtendPlanArgs p{};
   p.qsl = query_start_loc; p.seq_lens = seq_lens; p.prefix = prefix_lens;
+  p.num_tokens = (int)num_tokens;
   p.batch = batch; p.group = group; p.causal = causal ? 1 : 0; p.window = sliding_window < 0 ? -1 : sliding_window;
   p.tile_rows = bm;
   p.tile_keys = head_dim == 256 ? XShape<256>::BN : XShape<128>::BN;
@@ -731,6 +737,7 @@ extern "C" int ma_paged_extend(
   a.k = k_cache; a.v = v_cache; a.kv_stride_row = kv_stride_row; a.kv_stride_head = kv_stride_head;
   a.tt.table = table; a.tt.stride = table_stride; a.tt.page_shift = __builtin_ctz(page_size);
   a.row_index = row_index; a.seq_lens = seq_lens; a.qsl = query_start_loc; a.prefix = prefix_lens;
+  a.num_tokens = (int)num_tokens;
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group;
   a.items = p.items;
   a.causal = p.causal; a.window = p.window;

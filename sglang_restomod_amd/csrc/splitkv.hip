@@ -82,8 +82,9 @@ struct SplitKVArgs {
   const int32_t* seq_lens;   // keys visible to the last query row of each sequence
   const int32_t* qsl;        // [B+1] query start per sequence, or null (one row per sequence)
   const int32_t* prefix;     // [B] cached prefix per sequence, or null (seq_len - query count)
+  int num_tokens;            // rows of q and out: query rows are clamped into [0, num_tokens)
   int batch, hq, hkv, group;
-  int row_groups;            // row groups per (sequence, kv head) in the largest sequence
+  int row_groups;            // row groups per (sequence, kv head) at the host's longest-chain hint
   int rows;                  // rows per row group (16 * NB)
   int causal, window;
   float scale_log2;          // softmax_scale * k_scale * log2(e)
@@ -111,8 +112,9 @@ __device__ __forceinline__ Geom geom(const SplitKVArgs& a, int b) {
   g.b = b;
   g.seq = max(cptr(a.seq_lens)[b], 0);
   if (a.qsl) {
-    g.tok0 = cptr(a.qsl)[b];
-    g.ntok = cptr(a.qsl)[b + 1] - g.tok0;
+    const QueryRows qr = clamp_query_rows(cptr(a.qsl)[b], cptr(a.qsl)[b + 1], a.num_tokens);
+    g.tok0 = qr.tok0;
+    g.ntok = qr.ntok;
     g.prefix = a.prefix ? cptr(a.prefix)[b] : g.seq - g.ntok;
   } else {
     g.tok0 = b;
@@ -124,7 +126,7 @@ __device__ __forceinline__ Geom geom(const SplitKVArgs& a, int b) {
   g.span = g.seq - g.lo_min;
   g.nt = (g.span + (1 << TS) - 1) / (1 << TS);
   const int real_rows = max(g.ntok, 0) * a.group;
-  g.rg_real = min(a.row_groups, (real_rows + a.rows - 1) / a.rows);
+  g.rg_real = (int)(((int64_t)real_rows + a.rows - 1) / a.rows);  // every query row, whatever the host's hint
   g.seq_row = a.row_index ? cptr(a.row_index)[b] : (int64_t)b;
   return g;
 }
@@ -134,41 +136,50 @@ __device__ __forceinline__ Geom geom_u(const SplitKVArgs& a, int b) {
   return geom<TS>(a, __builtin_amdgcn_readfirstlane(b));
 }
 
-// tiles of sequence b over all its kv heads and row groups
+// tiles of sequence b over all its kv heads and row groups (64-bit: a verify sequence's
+// row groups are not capped, so rows x keys can pass 2^31)
 template <int TS>
-__device__ __forceinline__ int seq_work(const SplitKVArgs& a, int b) {
+__device__ __forceinline__ int64_t seq_work(const SplitKVArgs& a, int b) {
   const Geom g = geom<TS>(a, b);
-  return g.nt * g.rg_real * a.hkv;
+  return (int64_t)g.nt * g.rg_real * a.hkv;
 }
 
-__device__ __forceinline__ int shfl_up_i(int v, int delta) {
+__device__ __forceinline__ int64_t shfl_up_i64(int64_t v, int delta) {
   const int lane = lane_id();
-  const int src = lane >= delta ? lane - delta : lane;
-  return __builtin_amdgcn_ds_bpermute(src << 2, v);
+  const int src = (lane >= delta ? lane - delta : lane) << 2;
+  const int lo = __builtin_amdgcn_ds_bpermute(src, (int)(uint32_t)v);
+  const int hi = __builtin_amdgcn_ds_bpermute(src, (int)(v >> 32));
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 // Total tiles, and (when t >= 0) the sequence holding global tile t and t's offset in it.
 template <int TS>
-__device__ __forceinline__ void scan_work(const SplitKVArgs& a, int64_t t, int64_t& total, int& b_at, int& off_at) {
+__device__ __forceinline__ void scan_work(const SplitKVArgs& a, int64_t t, int64_t& total, int& b_at, int64_t& off_at) {
   const int lane = lane_id();
   int64_t base = 0;
   b_at = -1;
   off_at = 0;
   for (int b0 = 0; b0 < a.batch; b0 += 64) {
     const int b = b0 + lane;
-    const int w = b < a.batch ? seq_work<TS>(a, b) : 0;
-    int inc = w;
+    const int64_t w = b < a.batch ? seq_work<TS>(a, b) : 0;
+    int64_t inc = w;
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
-      const int y = shfl_up_i(inc, m);
+      const int64_t y = shfl_up_i64(inc, m);
       if (lane >= m) inc += y;
     }
-    const int chunk = __builtin_amdgcn_readlane(inc, 63);
+    const int64_t chunk = readlane_i64(inc, 63);
     if (b_at < 0 && t >= 0 && base + chunk > t) {
       const uint64_t hit = __builtin_amdgcn_ballot_w64(base + inc > t);
       const int L = __builtin_ctzll(hit);
       b_at = b0 + L;
-      off_at = (int)(t - (base + __builtin_amdgcn_readlane(inc - w, L)));
+      off_at = t - (base + readlane_i64(inc - w, L));
     }
     base += chunk;
   }
@@ -201,16 +212,21 @@ __device__ __forceinline__ int64_t scan_total(const SplitKVArgs& a, int W) {
   int64_t base = 0;
   for (int b0 = 0; b0 < a.batch; b0 += 64) {
     const int b = b0 + lane;
-    int w = 0;
+    int64_t w = 0;
     bool zero = false;
     if (b < a.batch) {
       const Geom g = geom<TS>(a, b);
-      w = g.nt * g.rg_real * a.hkv;
+      w = (int64_t)g.nt * g.rg_real * a.hkv;
       zero = g.nt == 0 && g.ntok > 0 && (b % a.nwaves) == W;
     }
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) w += __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, w);
-    base += __builtin_amdgcn_readfirstlane(w);
+    for (int m = 1; m < 64; m <<= 1) {
+      const int src = (lane ^ m) << 2;
+      const int lo = __builtin_amdgcn_ds_bpermute(src, (int)(uint32_t)w);
+      const int hi = __builtin_amdgcn_ds_bpermute(src, (int)(w >> 32));
+      w += (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+    }
+    base += readlane_i64(w, 0);
     uint64_t zm = __builtin_amdgcn_ballot_w64(zero);
     while (zm) {
       const int L = __builtin_ctzll(zm);
@@ -236,11 +252,11 @@ struct Cursor {
 };
 
 template <int TS>
-__device__ __forceinline__ void cursor_at(const SplitKVArgs& a, Cursor& c, int b, int off) {
+__device__ __forceinline__ void cursor_at(const SplitKVArgs& a, Cursor& c, int b, int64_t off) {
   c.g = geom_u<TS>(a, b);
   const int per_seg = c.g.nt;
-  const int seg = off / per_seg;
-  c.tile = off - seg * per_seg;
+  const int seg = (int)(off / per_seg);  // < rg_real * hkv
+  c.tile = (int)(off - (int64_t)seg * per_seg);
   c.h = seg / c.g.rg_real;
   c.rg = seg - c.h * c.g.rg_real;
   c.t = 0;
@@ -261,7 +277,7 @@ __device__ __forceinline__ void cursor_next(const SplitKVArgs& a, Cursor& c, int
   do {
     ++b;
     c.g = geom_u<TS>(a, b);
-  } while (c.g.nt * c.g.rg_real == 0);
+  } while (c.g.nt == 0 || c.g.rg_real == 0);
 }
 
 template <bool BF16>
@@ -311,6 +327,9 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   constexpr int kSMax = 63 / OPS + 1;
   constexpr int S = (kFp8 || D == 64) ? (kSMax < 8 ? kSMax : 8) : (kSMax < 4 ? kSMax : 4);
   constexpr int A = 2 * S - 3;  // slots are looked up A tiles ahead of compute
+  // Tiles kept in flight through a 16-bit tile's compute: none. Measured on decode and
+  // verify with whole-row nontemporal loads, keeping 1, 2 or 3 in flight is 2-3% slower.
+  constexpr int kInFlight16 = 0;
   static_assert(S >= 2 && (S - 1) * OPS <= 63, "more outstanding loads than the counter holds");
   static_assert(kVL >= 1 && 64 % kCPR == 0, "a V load covers whole rows");
 
@@ -344,7 +363,8 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     if (lane == 0) my_desc[0] = 0;
     return;
   }
-  int b0, off0;
+  int b0;
+  int64_t off0;
   {
     int64_t tot_again;
     scan_work<kTS>(a, t0, tot_again, b0, off0);
@@ -754,7 +774,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       // tiles stay in flight, which is 12% faster than waiting for all (3 to 7 tiles
       // in flight measured the same). With S = 2 (16-bit KV at D=256) the wait for the
       // slot above has already drained tile n, and tile n+1 stays in flight.
-      wait_vm(std::integral_constant<int, (kFp8 || S < 4) ? (S - 1) * OPS : 0>{});
+      wait_vm(std::integral_constant<int, (kFp8 || S < 4) ? (S - 1) * OPS : kInFlight16 * OPS>{});
       touch_k(ring[I]);
       compute(cc, ring[I], I);
       const bool seg_last = (cc.tile == cc.g.nt - 1);
@@ -982,6 +1002,7 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
       ((a.q_stride_head * 2) & 15) || ((a.out_stride_tok * 2) & 7) || ((a.out_stride_head * 2) & 7))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   a.group = a.hq / a.hkv;
+  if ((int64_t)a.num_tokens * a.group > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens x GQA group exceeds 2^31");
   const int rows_total = max_q_per_seq * a.group;
   const int nb = (rows_total <= 16 || head_dim == 256) ? 1 : 2;
   a.rows = 16 * nb;
@@ -1024,6 +1045,7 @@ extern "C" int ma_grouped_decode(
   a.k = k_cache; a.v = v_cache; a.kv_stride_row = kv_stride_row; a.kv_stride_head = kv_stride_head;
   a.tt.table = table; a.tt.stride = table_stride; a.tt.page_shift = __builtin_ctz(page_size);
   a.row_index = row_index; a.seq_lens = seq_lens; a.qsl = nullptr; a.prefix = nullptr;
+  a.num_tokens = batch;
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads;
   a.causal = 1; a.window = sliding_window < 0 ? -1 : sliding_window;
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
@@ -1041,7 +1063,7 @@ extern "C" int ma_paged_verify(
     int causal, int sliding_window, int num_workgroups,
     float softmax_scale, float k_scale, float v_scale, void* workspace, size_t workspace_bytes,
     void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
-  (void)num_tokens;
+  if (num_tokens < 0 || num_tokens > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens %lld out of range", (long long)num_tokens);
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
   if (!query_start_loc) return set_error(MA_EINVAL, "query_start_loc is required");
   if (max_q_per_seq > 64) return set_error(MA_EUNSUPPORTED, "verify supports at most 64 query rows per sequence");
@@ -1050,6 +1072,7 @@ extern "C" int ma_paged_verify(
   a.k = k_cache; a.v = v_cache; a.kv_stride_row = kv_stride_row; a.kv_stride_head = kv_stride_head;
   a.tt.table = table; a.tt.stride = table_stride; a.tt.page_shift = __builtin_ctz(page_size);
   a.row_index = row_index; a.seq_lens = seq_lens; a.qsl = query_start_loc; a.prefix = prefix_lens;
+  a.num_tokens = (int)num_tokens;
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads;
   a.causal = causal ? 1 : 0; a.window = sliding_window < 0 ? -1 : sliding_window;
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;

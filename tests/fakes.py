@@ -84,6 +84,10 @@ class TokenToKVPool:
 
     def set_kv_buffer(self, layer, loc, cache_k, cache_v, k_scale=None, v_scale=None):
         self.writes += 1
+        if getattr(self, "full_to_swa_index_mapping", None) is not None and \
+                getattr(layer, "sliding_window_size", -1) is not None and getattr(layer, "sliding_window_size", -1) >= 0:
+            # an SWA pool stores its sliding-window layers at their SWA slots
+            loc = self.full_to_swa_index_mapping[loc]
         if cache_k.dtype != self.dtype:
             if k_scale is not None:
                 cache_k = cache_k / k_scale

@@ -129,6 +129,64 @@ def test_draft_extend_routes_by_row_count(rows, mode):
     assert be.forward_metadata.mode == mode
 
 
+def test_draft_extend_routing_reads_no_device_value():
+    """Without extend_seq_lens_cpu the route comes from the token and request counts, and
+    the kernel's row-group hint from the token count; no device tensor is read."""
+    eng = _engine(spec="EAGLE", draft_worker=True)
+    eng.alloc(0, 50)
+    eng.alloc(1, 60)
+    be = _backend(eng)
+    fb = eng.batch("DRAFT_EXTEND", [0, 1], new_tokens=[3, 2])
+    del fb.extend_seq_lens_cpu
+
+    class NoHostRead(torch.Tensor):
+        def item(self):
+            raise AssertionError("a device value was read on the host")
+
+    fb.extend_seq_lens = fb.extend_seq_lens.as_subclass(NoHostRead)
+    be.init_forward_metadata(fb)
+    md = be.forward_metadata
+    assert md.mode == "verify" and md.max_q_per_seq == 5  # 5 tokens in all: a bound of the longest chain
+    assert md.query_start_loc.tolist() == [0, 3, 5]
+
+
+@pytest.mark.parametrize("mode", ["DRAFT_EXTEND", "DRAFT_EXTEND_V2"])
+def test_captured_draft_extend_is_refused(mode):
+    """The graph API does not say how many rows each request has in a draft extend; the
+    backend refuses to capture or replay one rather than guessing (a wrong guess would
+    send the kernels past q and out)."""
+    eng = _engine(spec="EAGLE", draft_worker=True)
+    for r in range(3):
+        eng.alloc(r, 40 + r)
+    be = _backend(eng)
+    be.init_cuda_graph_state(max_bs=4, max_num_tokens=16)
+    fm = fakes.ForwardMode(mode)
+    spec = type("S", (), {"num_tokens_per_req": 4, "draft_token_num": 4})()
+    rpi, seq = torch.tensor([0, 1, 2]), torch.tensor([40, 41, 42])
+    with pytest.raises(NotImplementedError, match="draft-extend graphs"):
+        be.init_forward_metadata_capture_cuda_graph(3, 12, rpi, seq, None, fm, spec)
+    with pytest.raises(NotImplementedError, match="draft-extend graphs"):
+        be.init_forward_metadata_replay_cuda_graph(3, rpi, seq, 123, None, fm, spec, None)
+
+
+def test_paged_forward_keeps_the_reference_signature():
+    """Positional order and defaults of the reference's paged_forward
+    (_paged_adapter.py:567-586); the extra keywords come after them."""
+    import inspect
+
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    params = list(inspect.signature(ops.paged_forward).parameters.values())
+    ref = [("q", inspect.Parameter.empty), ("k_cache", inspect.Parameter.empty),
+           ("v_cache", inspect.Parameter.empty), ("block_table", inspect.Parameter.empty),
+           ("seq_lens", inspect.Parameter.empty), ("query_start_loc", inspect.Parameter.empty),
+           ("prefix_kv_lens", inspect.Parameter.empty), ("out", None), ("block_size", 16),
+           ("num_kv_heads", None), ("softmax_scale", None), ("causal", True), ("sliding_window_size", -1),
+           ("linear_verify", False), ("k_scale", 1.0), ("v_scale", 1.0), ("max_seq_len_hint", None),
+           ("logical_dense_kv", False)]
+    assert [(p.name, p.default) for p in params[:len(ref)]] == ref
+
+
 def test_graph_buffers_keep_their_addresses_across_replays():
     eng = _engine(spec="EAGLE")
     for r in range(4):
@@ -204,10 +262,15 @@ def test_sinks_are_refused():
                           save_kv_cache=False, sinks=torch.zeros(8))
 
 
-def test_forward_on_cpu_tensors_raises_instead_of_falling_back():
+@pytest.mark.parametrize("native_write", ["1", "0"])
+def test_forward_on_cpu_tensors_raises_instead_of_falling_back(native_write, monkeypatch):
+    """The KV write and the attention both need device tensors: with the native write
+    (the default) the write itself refuses; with the pool's own write the attention does."""
+    monkeypatch.setenv("SGLANG_MI355X_NATIVE_KV_WRITE", native_write)
     eng = _engine()
     eng.alloc(0, 4)
     be = _backend(eng)
+    assert be.native_kv_write == (native_write == "1")
     fb = eng.batch("DECODE", [0], new_tokens=[1])
     be.init_forward_metadata(fb)
     layer = fakes.Layer(tp_q_head_num=8, tp_k_head_num=2)
@@ -215,7 +278,7 @@ def test_forward_on_cpu_tensors_raises_instead_of_falling_back():
     k = torch.zeros(1, 2, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="device tensors"):
         be.forward_decode(q, k, k.clone(), layer, fb)
-    assert eng.pool.writes == 1  # the new token's K/V was written first
+    assert eng.pool.writes == (0 if native_write == "1" else 1)
 
 
 def test_forward_without_metadata_raises():

@@ -113,6 +113,35 @@ def test_attest_write(tmp_path, monkeypatch):
     attest.reset()
 
 
+def test_attest_failure_after_inactive_and_list_order():
+    attest.reset()
+    attest.set_selected(["p", "q", "r"])
+    attest.record("q", True)
+    attest.inactive("p", "idle")
+    attest.record("p", False, "broke later")
+    attest.record("r", True, "fine")
+    snap = attest.snapshot()
+    assert snap["loaded"] == ["q", "r"] and snap["failed"] == ["p"] and snap["inactive"] == []
+    assert snap["components"] == {"q": {"ok": True}, "p": {"ok": False, "detail": "broke later"},
+                                  "r": {"ok": True, "detail": "fine"}}
+    assert set(snap) == {"engine", "selected", "components", "loaded", "failed", "inactive", "missing"}
+    attest.reset()
+
+
+def test_attest_write_leaves_only_the_target(tmp_path):
+    attest.reset()
+    attest.set_selected(["x"])
+    attest.inactive("x", object())
+    target = tmp_path / "att.json"
+    for _ in range(3):
+        assert attest.write(str(target)) == str(target)
+    assert [p.name for p in tmp_path.iterdir()] == ["att.json"]
+    doc = json.loads(target.read_text())
+    assert doc["inactive"] == ["x"] and doc["loaded"] == ["x"]
+    assert doc["components"]["x"]["detail"].startswith("registered, inactive: ")
+    attest.reset()
+
+
 def test_register_entry_point_writes_attest(tmp_path, monkeypatch):
     import sglang_restomod_amd
 
@@ -193,13 +222,6 @@ def test_cross_attention_is_not_causal():
 
 
 # ---- draft decode planning (reference KATs) --------------------------------
-
-def test_native_flag():
-    assert plan.native_enabled({}) is True
-    assert plan.native_enabled({plan.ENV_FLAG: "off"}) is False
-    with pytest.raises(ValueError, match=plan.ENV_FLAG):
-        plan.native_enabled({plan.ENV_FLAG: "maybe"})
-
 
 def test_page_table_reads_the_page_start_of_each_row():
     row0 = [0, 1, 2, 3, 12, 13, 14, 15, 8]

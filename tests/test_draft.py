@@ -1,5 +1,6 @@
-"""Draft-worker plumbing on the CPU: the factory patch, the launch gate, the multi-step
-container over a stand-in for the engine's container, and a step's metadata."""
+"""Draft-worker plumbing on the CPU: the factory routing, the support gate, the multi-step
+container's per-round rows (top-k 1 over req_to_token in place, graph buffers), and a
+pass's flat-list rows."""
 
 from __future__ import annotations
 
@@ -31,55 +32,76 @@ class Factory:
         return "engine-decode"
 
 
-def _patched(native="native"):
+def _rerouted(container="container"):
     cls = type("F", (Factory,), {})
-    built = []
+    built, made = [], []
     wrapped = SimpleNamespace()
-    changed = draft_backend.install_on(
-        cls, build=lambda r: built.append(r) or "backend", wrap=lambda r, b: wrapped,
-        build_native=lambda r, topk, steps, stamp: native)
-    return cls, built, wrapped, changed
+
+    def build_container(runner, topk, steps, name):
+        made.append((runner, topk, steps, name))
+        if isinstance(container, Exception):
+            raise container
+        return container
+
+    changed = draft_backend.install_on(cls, build=lambda r: built.append(r) or "backend", wrap=lambda r, b: wrapped,
+                                       build_container=build_container)
+    return cls, built, wrapped, made, changed
 
 
 def test_other_names_keep_the_engine_backends():
-    cls, built, _, _ = _patched()
+    cls, built, _, made, _ = _rerouted()
     f = cls("triton")
     assert f.create_draft_extend_backend() == "engine-extend"
     assert f.create_decode_backend() == "engine-decode"
-    assert built == []
+    assert built == [] and made == []
 
 
 def test_draft_extend_gets_the_backend_wrapped_and_stamped():
-    cls, built, wrapped, changed = _patched()
+    cls, built, wrapped, _, changed = _rerouted()
     assert changed
     f = cls("mi355x_attn")
     assert f.create_draft_extend_backend() is wrapped
     assert built == ["runner"]
     assert wrapped.prefill_attention_backend_str == "mi355x_attn"
+    assert wrapped.decode_attention_backend_str == "mi355x_attn"
 
 
-def test_draft_decode_gets_the_native_container():
-    cls, _, _, _ = _patched(native="native-container")
-    assert cls("mi355x_attn", steps=3).create_decode_backend() == "native-container"
+def test_draft_decode_gets_the_split_kv_container():
+    cls, _, _, made, _ = _rerouted(container="native-container")
+    assert cls("mi355x_attn", steps=3, topk=2).create_decode_backend() == "native-container"
+    assert made == [("runner", 2, 3, "mi355x_attn")]
 
 
-def test_unsupported_draft_decode_falls_back_and_restores_the_name():
-    cls, _, _, _ = _patched(native=None)
+def test_unservable_draft_decode_raises_instead_of_rerouting():
+    cls, _, _, _, _ = _rerouted(container=NotImplementedError("no"))
     f = cls("mi355x_attn", steps=3)
-    assert f.create_decode_backend() == "engine-decode"
-    assert f.calls[-1] == ("decode", "triton")
+    with pytest.raises(NotImplementedError):
+        f.create_decode_backend()
+    assert f.calls == []  # nothing was handed to the engine's own backends
     assert f.draft_attn_backend == "mi355x_attn"
 
 
-def test_single_step_draft_uses_the_engine_decode():
-    cls, _, _, _ = _patched()
+def test_single_step_draft_uses_the_engine_method():
+    cls, _, _, made, _ = _rerouted()
     f = cls("mi355x_attn", steps=1)
     assert f.create_decode_backend() == "engine-decode"
+    assert made == []
 
 
-def test_patching_twice_changes_nothing():
-    cls, _, _, _ = _patched()
+def test_rerouting_twice_changes_nothing_and_uninstall_restores():
+    cls, _, _, _, _ = _rerouted()
     assert draft_backend.install_on(cls, build=None, wrap=None) is False
+    assert draft_backend.uninstall(cls) is True
+    assert cls("mi355x_attn").create_decode_backend() == "engine-decode"
+    assert draft_backend.uninstall(cls) is False
+
+
+def test_no_triton_anywhere_in_the_package():
+    import pathlib
+
+    pkg = pathlib.Path(draft_backend.__file__).resolve().parents[2]
+    hits = [str(p) for p in pkg.rglob("*") if p.suffix in (".py", ".hip", ".h") and "triton" in p.read_text().lower()]
+    assert hits == []
 
 
 def _runner(**over):
@@ -94,104 +116,101 @@ def _runner(**over):
 LAYERS = [fakes.Layer(8, 2)]
 
 
-@pytest.mark.parametrize("over,env,window,layers,reason", [
-    ({}, {"SGLANG_MI355X_DRAFT_DECODE_NATIVE": "0"}, (0, 0), LAYERS, "disabled_by_env"),
-    ({"page_size": 16}, {}, (0, 0), LAYERS, "page_size"),
-    ({"kv_cache_dtype": torch.float32}, {}, (0, 0), LAYERS, "kv_dtype"),
-    ({}, {}, (128, 0), LAYERS, "draft_window"),
-    ({"sliding_window_size": 512}, {}, (0, 0), LAYERS, "draft_sliding_window"),
-    ({"kv_index_translator": SimpleNamespace(is_translating=True)}, {}, (0, 0), LAYERS, "kv_index_translation"),
-    ({}, {}, (0, 0), [], "no_attention_layers"),
-    ({}, {}, (0, 0), [fakes.Layer(8, 2, head_dim=96)], "head_dim"),
+@pytest.mark.parametrize("over,topk,window,layers,gap", [
+    ({"page_size": 16}, 2, (0, 0), LAYERS, "page size 16"),
+    ({"kv_cache_dtype": torch.float32}, 1, (0, 0), LAYERS, "KV cache dtype"),
+    ({}, 1, (128, 0), LAYERS, "draft-decode window"),
+    ({}, 1, (0, 4), LAYERS, "sink=4"),
+    ({"kv_index_translator": SimpleNamespace(is_translating=True)}, 1, (0, 0), LAYERS, "KV index translation"),
+    ({}, 1, (0, 0), [fakes.Layer(8, 2, head_dim=96)], "head_dim(96)"),
+    ({}, 1, (0, 0), [fakes.Layer(8, 3)], "gqa_ratio"),
 ])
-def test_unsupported_reasons(over, env, window, layers, reason):
-    got = draft_decode.unsupported_reason(_runner(**over), 1, env=env, draft_window=window, layers=layers)
-    assert got is not None and reason in got
+def test_support_gaps(over, topk, window, layers, gap):
+    gaps = draft_decode.support_gaps(_runner(**over), topk, window, layers)
+    assert any(gap in g for g in gaps), gaps
+    with pytest.raises(NotImplementedError, match="cannot serve this draft worker"):
+        draft_decode.MI355XMultiStepDraftBackend(_runner(**over), topk, 3, draft_window=window, layers=layers)
 
 
-def test_supported_launch_has_no_reason():
-    assert draft_decode.unsupported_reason(_runner(), 1, env={}, layers=LAYERS) is None
+@pytest.mark.parametrize("over,topk", [({}, 1), ({"page_size": 16}, 1), ({}, 4), ({"sliding_window_size": 512}, 1)])
+def test_servable_draft_workers(over, topk):
+    assert draft_decode.support_gaps(_runner(**over), topk, (0, 0), LAYERS) == []
 
 
-def test_swa_pool_is_refused():
+def test_swa_pool_is_served():
     eng = fakes.Engine("cpu", swa=True)
     eng.runner.model_config.dtype = torch.bfloat16
-    assert draft_decode.unsupported_reason(eng.runner, 1, env={}, layers=LAYERS) == "swa_kv_pool"
+    assert draft_decode.support_gaps(eng.runner, 1, (0, 0), LAYERS) == []
 
 
-class EngineContainer:
-    """Stand-in for the engine's TritonMultiStepDraftBackend."""
-
-    def __init__(self, model_runner, topk, speculative_num_steps):
-        self.max_context_len = 2048
-        self.speculative_num_steps = speculative_num_steps
-        self.topk = topk
-        self.templates = []
-
-    def common_template(self, forward_batch, kv_indices_buffer, call_fn):
-        self.templates.append(forward_batch)
-        for step in range(self.speculative_num_steps - 1):
-            call_fn(step, forward_batch)
-
-    def init_forward_metadata_out_graph(self, forward_batch, in_capture=False):
-        return "captured"
+def _container(steps=4, topk=1, **eng_kw):
+    eng = fakes.Engine("cpu", **eng_kw)
+    eng.runner.model_config.dtype = torch.bfloat16
+    return eng, draft_decode.MI355XMultiStepDraftBackend(eng.runner, topk, steps, layers=LAYERS)
 
 
-def test_container_has_split_kv_children_and_replays_through_the_template():
-    runner = _runner()
-    runner.model = SimpleNamespace(modules=lambda: list(LAYERS))
-    cont = draft_decode.build_native(runner, 1, 4, "mi355x_attn", base_cls=EngineContainer)
-    assert len(cont.attn_backends) == 3
-    assert all(isinstance(c, draft_decode.MI355XDraftDecodeBackend) for c in cont.attn_backends)
-    assert cont.decode_attention_backend_str == "mi355x_attn"
-    indptr = torch.tensor([0, 3, 5], dtype=torch.int32)
-    indices = torch.tensor([7, 8, 9, 1, 2], dtype=torch.int32)
-    fb = SimpleNamespace(spec_info=SimpleNamespace(kv_indptr=indptr, kv_indices=indices))
-    assert cont.init_forward_metadata_out_graph(fb, in_capture=True) == "captured"
-    cont.init_forward_metadata_out_graph(fb, in_capture=False)
-    assert cont.templates == [fb]
-    assert all(c._rows_used == 2 for c in cont.attn_backends)
+def test_container_children_and_stamps():
+    _, cont = _container(steps=4)
+    assert len(cont.attn_backends) == 3 and cont.passes == 3
+    assert [c.step for c in cont.attn_backends] == [0, 1, 2]
+    assert all(c.decode_attention_backend_str == "mi355x_attn" for c in (cont, *cont.attn_backends))
 
 
-def test_step_metadata_reads_the_flat_list_in_place():
-    runner = _runner()
-    step = draft_decode.MI355XDraftDecodeBackend(runner, 2, 2048, 1, 3)
+def test_top1_round_reads_req_to_token_in_place():
+    """With one branch the draft tokens follow the prefix in req_to_token, so every pass
+    reads the request's own row: pass i sees seq_len + i + 1 keys."""
+    eng, cont = _container(steps=4, topk=1)
+    fb = SimpleNamespace(req_pool_indices=torch.tensor([3, 1]), seq_lens=torch.tensor([10, 25]), batch_size=2,
+                         seq_lens_cpu=torch.tensor([10, 25]))
+    cont.init_forward_metadata(fb)
+    rows = cont.current
+    assert rows.table is eng.req_to_token
+    assert rows.row_index.tolist() == [3, 1]
+    assert rows.lens.tolist() == [[11, 26], [12, 27], [13, 28]]
+    assert rows.swa_table is None
+    assert all(c.rows() is rows for c in cont.attn_backends)
+
+
+def test_graph_round_keeps_buffer_addresses():
+    _, cont = _container(steps=3, topk=1)
+    cont.init_cuda_graph_state(max_bs=4, max_num_tokens=4)
+    fb = SimpleNamespace(req_pool_indices=torch.tensor([0, 2, 1]), seq_lens=torch.tensor([5, 6, 7]), batch_size=3)
+    cont.init_forward_metadata_capture_cuda_graph(fb)
+    ptrs = (cont.current.row_index.data_ptr(), cont.current.lens.data_ptr())
+    fb2 = SimpleNamespace(req_pool_indices=torch.tensor([1, 0, 2]), seq_lens=torch.tensor([9, 3, 4]), batch_size=3)
+    cont.init_forward_metadata_replay_cuda_graph(fb2, 3)
+    assert (cont.current.row_index.data_ptr(), cont.current.lens.data_ptr()) == ptrs
+    assert cont.current.row_index.tolist() == [1, 0, 2]
+    assert cont.current.lens.tolist() == [[10, 4, 5], [11, 5, 6]]
+    with pytest.raises(ValueError, match="capacity"):
+        cont.plan(torch.arange(5), torch.ones(5, dtype=torch.int32), graph=True)
+
+
+def test_flat_list_rows_are_read_in_place():
     indptr = torch.tensor([0, 4, 4, 7], dtype=torch.int32)
     indices = torch.tensor([5, 6, 7, 8, 10, 11, 12], dtype=torch.int32)
-    assert step.refresh(indptr, indices) == 3
-    assert step._row_index.tolist() == [0, 4, 4] and step._row_index.dtype == torch.int64
-    assert step._seq_lens.tolist() == [4, 0, 3] and step._seq_lens.dtype == torch.int32
+    rows = draft_decode.DraftRows.from_flat_lists(indptr, indices)
+    assert rows.rows == 3
+    assert rows.row_index.tolist() == [0, 4, 4] and rows.row_index.dtype == torch.int64
+    assert rows.lens.tolist() == [[4, 0, 3]] and rows.lens.dtype == torch.int32
     # position p of row r is table[row_index[r] * 1 + p]
-    assert step._table.stride() == (1, 1) and step._table.data_ptr() == indices.data_ptr()
-    assert [int(step._table[int(step._row_index[2]) + p, 0]) for p in range(3)] == [10, 11, 12]
+    assert rows.table.stride() == (1, 1) and rows.table.data_ptr() == indices.data_ptr()
+    assert [int(rows.table[int(rows.row_index[2]) + p, 0]) for p in range(3)] == [10, 11, 12]
 
 
-def test_step_metadata_in_graph_buffers_keeps_addresses():
-    runner = _runner()
-    step = draft_decode.MI355XDraftDecodeBackend(runner, 1, 2048, 1, 3)
-    step.init_cuda_graph_state(max_bs=4, max_num_tokens=4)
-    step.refresh(torch.tensor([0, 2, 5], dtype=torch.int32), torch.arange(5, dtype=torch.int32))
-    p = (step._row_index.data_ptr(), step._seq_lens.data_ptr())
-    step.refresh(torch.tensor([0, 1, 2], dtype=torch.int32), torch.arange(2, dtype=torch.int32))
-    assert (step._row_index.data_ptr(), step._seq_lens.data_ptr()) == p
-    assert step._seq_lens.tolist() == [1, 1]
-    with pytest.raises(ValueError, match="capacity"):
-        step.refresh(torch.arange(7, dtype=torch.int32), torch.arange(6, dtype=torch.int32))
-
-
-def test_step_sizes_its_workspace_for_the_model_head_dim():
-    """The split-KV workspace grows with the head dim, so a step takes the model's
-    (and the largest supported one when the runner gives no model config)."""
-    runner = _runner()
-    runner.model_config.head_dim = 256
-    assert draft_decode.MI355XDraftDecodeBackend(runner, 1, 2048, 1, 3).head_dim == 256
-    bare = SimpleNamespace(**{k: v for k, v in vars(_runner()).items() if k != "model_config"})
-    step = draft_decode.MI355XDraftDecodeBackend(bare, 1, 2048, 1, 3)
-    assert step.head_dim == max(draft_decode_plan.SUPPORTED_HEAD_DIMS)
-
-
-def test_step_refuses_mismatched_rows():
-    step = draft_decode.MI355XDraftDecodeBackend(_runner(), 1, 2048, 1, 3)
-    step.refresh(torch.tensor([0, 2], dtype=torch.int32), torch.arange(2, dtype=torch.int32))
+def test_pass_refuses_mismatched_rows():
+    _, cont = _container(steps=3)
+    cont.attn_backends[0].use_flat_lists(torch.tensor([0, 2], dtype=torch.int32), torch.arange(2, dtype=torch.int32))
     with pytest.raises(RuntimeError, match="rows"):
-        step.forward_decode(torch.zeros(3, 8 * 128), None, None, fakes.Layer(8, 2), None, save_kv_cache=False)
+        cont.attn_backends[0].forward_decode(torch.zeros(3, 8 * 128), None, None, fakes.Layer(8, 2), None,
+                                             save_kv_cache=False)
+
+
+def test_container_sizes_its_workspace_for_the_model_head_dim():
+    eng = fakes.Engine("cpu", head_dim=256)
+    eng.runner.model_config.dtype = torch.bfloat16
+    cont = draft_decode.MI355XMultiStepDraftBackend(eng.runner, 1, 3, layers=[fakes.Layer(8, 2, head_dim=256)])
+    assert cont.head_dim == 256
+    bare = SimpleNamespace(**{k: v for k, v in vars(_runner()).items() if k != "model_config"})
+    assert draft_decode.MI355XMultiStepDraftBackend(bare, 1, 3, layers=LAYERS).head_dim == \
+        max(draft_decode_plan.SUPPORTED_HEAD_DIMS)

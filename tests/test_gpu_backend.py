@@ -132,8 +132,7 @@ def test_sliding_window_layer_through_swa_pool():
     # the SWA layer's K/V live at the translated slots of the same pool (a stand-in for
     # the separate SWA pool): write them there, then attend through the swa table
     swa = fakes.Layer(HQ, HKV, layer_id=0, sliding_window_size=64)
-    mapped = eng.pool.full_to_swa_index_mapping[fb.out_cache_loc]
-    eng.pool.set_kv_buffer(swa, mapped, k, v)
+    eng.pool.set_kv_buffer(swa, fb.out_cache_loc, k, v)  # the pool maps them to SWA slots
     out = be.forward_extend(q, k, v, swa, fb, save_kv_cache=False)
     kp, vp = _pools(eng)
     swa_r2t = eng.pool.full_to_swa_index_mapping[eng.req_to_token.long()].cpu().numpy()

@@ -57,8 +57,8 @@ def _workload_extend(gpu, batch=None, scale_lens=1.0, sample=None, kv_format=Non
     print(f"[case] extend {w.name} batch={w.batch} kv={w.k_pool.dtype}", flush=True)
     qsl = w.query_start_loc
     E = w.extend_lens.tolist()
-    out = _ops().paged_forward(
-        w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens,
+    out, _ = _ops().paged_forward(
+        w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens, block_size=1,
         softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale, causal=True,
         row_index=w.req_pool_indices, max_seq_len_hint=max(w.seq_lens_cpu), max_q_len_hint=max(E))
     torch.cuda.synchronize()
@@ -117,7 +117,7 @@ def _run_synthetic(gpu, prefix, extend, heads, heads_kv, causal=True, window=-1,
     if page_size > 1:
         kc = k.view(-1, page_size, heads_kv, dim)
         vc = v.view(-1, page_size, heads_kv, dim)
-    out = _ops().paged_forward(
+    out, _ = _ops().paged_forward(
         q, kc, vc, table.to(gpu), torch.tensor(seq, dtype=torch.int32, device=gpu),
         torch.tensor(qsl, dtype=torch.int32, device=gpu), torch.tensor(prefix, dtype=torch.int32, device=gpu),
         softmax_scale=scale, causal=causal, sliding_window_size=window, block_size=page_size,
@@ -261,3 +261,32 @@ def test_extend_in_a_hip_graph_replays_new_splits():
         rows_of = {b: list(range(extend[b])) for b in range(B)}
         _check_rows(qs, k, v, lambda b, n: oracle.slots_from_page_table(t, b, n, 1), prefix, qsl, got,
                     rows_of, 128 ** -0.5, what=f"replay {it}")
+
+
+def test_paged_forward_with_the_reference_call_shape(gpu):
+    """The reference's callers pass the seven tensors positionally, rely on block_size=16
+    with a [pages, 16, Hkv, D] cache, and unpack (out, softmax_lse)
+    (_paged_adapter.py:567-586, :756-759)."""
+    prefix, extend, heads, heads_kv = [40, 0, 200], [30, 17, 64], 16, 4
+    q, k, v, table, seq, qsl = _synthetic(gpu, prefix, extend, heads, heads_kv, page_size=16)
+    kc, vc = k.view(-1, 16, heads_kv, 128), v.view(-1, 16, heads_kv, 128)
+    print("[case] paged_forward reference call shape", flush=True)
+    out, lse = _ops().paged_forward(
+        q, kc, vc, table.to(gpu), torch.tensor(seq, dtype=torch.int32, device=gpu),
+        torch.tensor(qsl, dtype=torch.int32, device=gpu), torch.tensor(prefix, dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and out.dtype == q.dtype
+    assert lse.shape == (heads, sum(extend)) and lse.dtype == torch.float32
+    t = table.numpy()
+    rows_of = {b: list(range(extend[b])) for b in range(len(prefix))}
+    _check_rows(q, k, v, lambda b, n: oracle.slots_from_page_table(t, b, n, 16), prefix, qsl, out, rows_of,
+                128 ** -0.5, what="reference call shape")
+    # the same batch as a linear verify (few rows per sequence) also returns the pair
+    out2, lse2 = _ops().paged_forward(
+        q, kc, vc, table.to(gpu), torch.tensor(seq, dtype=torch.int32, device=gpu),
+        torch.tensor(qsl, dtype=torch.int32, device=gpu), torch.tensor(prefix, dtype=torch.int32, device=gpu),
+        linear_verify=True)
+    torch.cuda.synchronize()
+    assert lse2.shape == lse.shape
+    _check_rows(q, k, v, lambda b, n: oracle.slots_from_page_table(t, b, n, 16), prefix, qsl, out2, rows_of,
+                128 ** -0.5, what="reference call shape, verify route")
