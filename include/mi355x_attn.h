@@ -107,6 +107,28 @@ int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
                       int64_t out_stride_head, void* stream);
 
 /*
+ * Allocation-free variant of ma_grouped_decode. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory, not even a workspace (code under HIP graph
+ * capture that may not call hipMalloc, tight serving loops, harnesses that forbid it).
+ * Same arguments and results as ma_grouped_decode minus the workspace: the split-KV
+ * partials go to a static scratch array in the library's device code (one copy per GPU,
+ * held from the library's first use on that GPU until the process ends) sized for
+ * num_workgroups <= MA_NOALLOC_MAX_WORKGROUPS at head_dim <= 256: 67,403,776 bytes.
+ * Larger grids return MA_EINVAL. Nothing is allocated or freed; the scratch needs no
+ * clearing (every call rewrites what it reads). Calls that overlap in time on one GPU
+ * (two streams) share the scratch and race: serialise them.
+ */
+#define MA_NOALLOC_MAX_WORKGROUPS 256
+int ma_grouped_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
+                              const void* k_cache, const void* v_cache, int64_t kv_stride_row,
+                              int64_t kv_stride_head, int kv_dtype, const int32_t* table,
+                              int64_t table_stride, const int64_t* row_index, int page_size,
+                              const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
+                              int head_dim, int num_workgroups, float softmax_scale, float k_scale,
+                              float v_scale, int sliding_window, void* out, int64_t out_stride_tok,
+                              int64_t out_stride_head, void* stream);
+
+/*
  * Grouped split-KV verify: a few query tokens per sequence (linear speculative
  * chain), query row i of sequence b seeing keys j <= prefix_lens[b] + i when causal.
  * Replaces the linear_verify branch of paged_forward

@@ -23,6 +23,9 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.
 
 MA_DT_F16, MA_DT_BF16, MA_DT_E4M3, MA_DT_E5M2 = 0, 1, 2, 3
 MA_OK = 0
+MA_EINVAL, MA_ELAUNCH, MA_EUNSUPPORTED = -1, -2, -3
+# grid limit of ma_grouped_decode_noalloc's static scratch (include/mi355x_attn.h)
+MA_NOALLOC_MAX_WORKGROUPS = 256
 
 # name -> (restype, argtypes); the header is the source of truth.
 SIGNATURES = {
@@ -38,6 +41,14 @@ SIGNATURES = {
         c_void_p, c_int, c_int, c_int, c_int,         # seq_lens, batch, hq, hkv, dim
         c_int, c_float, c_float, c_float,             # num_workgroups, scales
         c_int, c_void_p, c_size_t,                    # window, workspace, bytes
+        c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
+    ]),
+    "ma_grouped_decode_noalloc": (c_int, [
+        c_void_p, c_int64, c_int64, c_int,            # q, strides, dtype
+        c_void_p, c_void_p, c_int64, c_int64, c_int,  # k, v, row/head stride, kv dtype
+        c_void_p, c_int64, c_void_p, c_int,           # table, stride, row_index, page size
+        c_void_p, c_int, c_int, c_int, c_int,         # seq_lens, batch, hq, hkv, dim
+        c_int, c_float, c_float, c_float, c_int,      # num_workgroups, scales, window
         c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
     ]),
     "ma_paged_verify": (c_int, [

@@ -48,6 +48,7 @@
 // at the wave's last tile, so the pipelined loop has no data-dependent branches around
 // loads and the counts stay exact.
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -959,19 +960,58 @@ static int device_workgroups(int requested) {
 // [LSE: nwaves x 2 x 32 fp32], each region 256-byte aligned. Every call rewrites the
 // descriptors of all its waves, so the workspace needs no initialisation.
 constexpr int kMaxWorkgroups = 16384;
-static size_t ws_desc_bytes(int num_workgroups) {
+static constexpr size_t ws_desc_bytes(int num_workgroups) {
   return ((size_t)num_workgroups * kWaves * kDescInts * sizeof(int) + 255) & ~(size_t)255;
 }
-static size_t ws_o_bytes(int num_workgroups, int head_dim) {
+static constexpr size_t ws_o_bytes(int num_workgroups, int head_dim) {
   const size_t pieces = (size_t)num_workgroups * kWaves * 2 * kMaxRows;
   return (pieces * head_dim * sizeof(float) + 255) & ~(size_t)255;
 }
 
+static constexpr size_t ws_bytes(int num_workgroups, int head_dim) {
+  return ws_desc_bytes(num_workgroups) + ws_o_bytes(num_workgroups, head_dim) +
+         (((size_t)num_workgroups * kWaves * 2 * kMaxRows * sizeof(float) + 255) & ~(size_t)255);
+}
+
 extern "C" size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim) {
   if (num_workgroups <= 0 || head_dim <= 0) return 0;
-  const size_t pieces = (size_t)num_workgroups * kWaves * 2 * kMaxRows;
-  return ws_desc_bytes(num_workgroups) + ws_o_bytes(num_workgroups, head_dim) +
-         ((pieces * sizeof(float) + 255) & ~(size_t)255);
+  return ws_bytes(num_workgroups, head_dim);
+}
+
+// ---------------------------------------------------------------------------
+// Static scratch of the allocation-free decode (ma_grouped_decode_noalloc): the split-KV
+// workspace of a persistent grid of up to kScratchWorkgroups workgroups at the largest
+// head dim, in device memory that the code object itself carries. Each device the
+// library runs on holds one copy from the module's load until the process ends. The
+// kernels never read this symbol: host code passes the copy's device address, taken once
+// per device with hipGetSymbolAddress (the name itself is a host-side stand-in, not a
+// device address).
+// ---------------------------------------------------------------------------
+constexpr int kScratchWorkgroups = MA_NOALLOC_MAX_WORKGROUPS;
+constexpr size_t kScratchBytes = ws_bytes(kScratchWorkgroups, 256);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// This device's copy of `scratch`, looked up on its first use with the device current.
+static int scratch_of_current_device(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(MA_ELAUNCH, "hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return set_error(MA_EUNSUPPORTED, "device %d beyond %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(MA_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MA_OK;
 }
 
 extern "C" int ma_device_workgroups(void) { return device_workgroups(0); }
@@ -1079,4 +1119,23 @@ extern "C" int ma_paged_verify(
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
   return splitkv_run(a, head_dim, q_dtype, kv_dtype, max_q_per_seq, num_workgroups, workspace, workspace_bytes,
                      (hipStream_t)stream);
+}
+
+extern "C" int ma_grouped_decode_noalloc(
+    const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
+    const void* k_cache, const void* v_cache, int64_t kv_stride_row, int64_t kv_stride_head, int kv_dtype,
+    const int32_t* table, int64_t table_stride, const int64_t* row_index, int page_size,
+    const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+    int num_workgroups, float softmax_scale, float k_scale, float v_scale, int sliding_window,
+    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+  if (num_workgroups <= 0 || num_workgroups > kScratchWorkgroups)
+    return set_error(MA_EINVAL, "num_workgroups %d: the static scratch serves 1..%d", num_workgroups, kScratchWorkgroups);
+  if (head_dim > 256) return set_error(MA_EUNSUPPORTED, "head_dim %d exceeds the static scratch's 256", head_dim);
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws);
+  if (rc != MA_OK) return rc;
+  return ma_grouped_decode(q, q_stride_tok, q_stride_head, q_dtype, k_cache, v_cache, kv_stride_row, kv_stride_head,
+                           kv_dtype, table, table_stride, row_index, page_size, seq_lens, batch, num_q_heads,
+                           num_kv_heads, head_dim, num_workgroups, softmax_scale, k_scale, v_scale, sliding_window, ws,
+                           kScratchBytes, out, out_stride_tok, out_stride_head, stream);
 }

@@ -193,3 +193,14 @@ def _g8_args(**over):
 def test_fp8_gather_rejects_bad_arguments(lib, over, msg):
     assert lib.ma_gather_fp8_paged_kv(*_g8_args(**over)) != 0
     assert msg in lib.ma_last_error().decode()
+
+
+def test_loader_constants_match_the_header():
+    import pathlib
+
+    from sglang_restomod_amd.attention.mi355x import _lib as L
+
+    hdr = (pathlib.Path(__file__).resolve().parents[1] / "include" / "mi355x_attn.h").read_text()
+    for name in ("MA_OK", "MA_EINVAL", "MA_ELAUNCH", "MA_EUNSUPPORTED", "MA_NOALLOC_MAX_WORKGROUPS"):
+        want = int(re.search(rf"#define {name} \(?(-?\d+)\)?", hdr).group(1))
+        assert getattr(L, name) == want, name
