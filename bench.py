@@ -1,17 +1,22 @@
 """Benchmark of the MI355X paged-attention hot path on one GPU.
 
-    python bench.py [--steps K] [--warmup W] [--workload N] [--secondary] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--workload N] [--headline-only] [--no-cpu-baseline]
 
 One step = one call of the hot path over one batch of synthetic input already
-resident in HBM:
+resident in HBM. The metric has two halves (decode GB/s against the HBM roofline,
+extend TFLOP/s against the bf16 MFMA roofline), so one JSON line carries:
 
-* workload 1 (default, the headline): batched ragged paged decode, B=64,
-  ctx U[1024, 8192], 64 q / 8 kv heads, D=128, bf16, page size 1 with shuffled
-  slots. ``value`` = algorithmic GB/s (K+V once per token and kv head, 4 B of
-  slot index per token, q in and out) over the timed region.
-* ``--secondary`` adds the other workloads (extend TFLOP/s, fp8 decode GB/s,
-  verify GB/s, and the KV write of an extend batch into an fp8 pool) as extra fields
-  of the same JSON line.
+* the headline, workload 1 (``value``, ``roofline``, ``cpu_baseline``): batched ragged
+  paged decode, B=64, ctx U[1024, 8192], 64 q / 8 kv heads, D=128, bf16, page size 1
+  with shuffled slots. ``value`` = algorithmic GB/s (K+V once per token and kv head,
+  4 B of slot index per token, q in and out) over the timed region;
+* ``extend``: workload 2, prefix-aware extend, B=8, P U[0, 4096], E U[256, 2048],
+  40 q / 8 kv heads, bf16: TFLOP/s of the visible query-key pairs (4 D Hq flop each),
+  its MFMA roofline and a CPU baseline;
+* ``fp8_decode``: workload 3 (B=128, ctx U[4096, 32768], 32 / 8 heads) over e4m3 and
+  e5m2 pools; ``verify``: workload 4 (B=32, 4 draft tokens, P U[2048, 16384], 64 / 8
+  heads); ``decode_b1``: workload 0's latency; ``kv_write``: the pool write of the
+  extend batch into an e4m3 pool. ``--headline-only`` skips all of these.
 
 ``value`` is whole-job throughput: algorithmic bytes of the K timed steps over
 the wall time between the two synchronisations. Warm-up is W untimed steps and
@@ -55,9 +60,13 @@ def _parse():
     p.add_argument("--workload", type=int, default=1)
     p.add_argument("--kv-format", choices=("e4m3", "e5m2"), default="e4m3",
                    help="fp8 format of workload 3's KV")
-    p.add_argument("--secondary", action="store_true")
+    p.add_argument("--headline-only", action="store_true",
+                   help="measure the headline workload only (default: every workload family)")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=20.0)
+    p.add_argument("--cpu-seconds", type=float, default=16.0,
+                   help="CPU budget of the headline's torch-native baseline")
+    p.add_argument("--cpu-seconds-secondary", type=float, default=10.0,
+                   help="CPU budget of each other workload's baseline")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     return p.parse_args()
 
@@ -189,53 +198,54 @@ def _time_gpu(fn, steps, warmup):
 
 
 def _cpu_baseline(w, budget_s):
-    """torch-native restatement on this host's cores, on a bounded sample of sequences."""
+    """torch-native restatement on this host's cores over a bounded sample of sequences:
+    the sample grows until one pass takes about a quarter of ``budget_s``, then the median
+    of up to three passes is kept. Returns (seconds, sequences, cores)."""
     import torch
 
     from oracle import torch_native as TN
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    B = w.batch
+    # the sequences in ascending order of size, so small samples stay small
+    order = sorted(range(B), key=lambda b: w.seq_lens_cpu[b])
     kc, vc = w.k_pool.cpu(), w.v_pool.cpu()
     qc = w.q.cpu()
     r2t, rpi = w.req_to_token.cpu(), w.req_pool_indices.cpu()
     seq = w.seq_lens.cpu()
-    B = w.batch
+    pre = w.prefix_lens.cpu().tolist()
+    ext = w.extend_lens.cpu().tolist()
+    qsl = [0]
+    for e in ext:
+        qsl.append(qsl[-1] + e)
 
     def run(rows):
         if w.mode == "decode":
             TN.decode(qc, kc, vc, r2t, rpi, seq, softmax_scale=w.softmax_scale, k_scale=w.k_scale,
                       v_scale=w.v_scale, batch_subset=rows)
         else:
-            pre = w.prefix_lens.cpu().tolist()
-            ext = w.extend_lens.cpu().tolist()
-            qsl = [0]
-            for e in ext:
-                qsl.append(qsl[-1] + e)
             sub_q = torch.cat([qc[qsl[b]:qsl[b + 1]] for b in rows])
             TN.extend(sub_q, kc, vc, r2t, rpi[rows], [pre[b] for b in rows], [ext[b] for b in rows],
-                      softmax_scale=w.softmax_scale)
+                      softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale)
 
-    # grow the sample until one pass takes a measurable share of the budget
     n = 1
-    t = 0.0
     while True:
-        rows = list(range(min(n, B)))
+        rows = sorted(order[:n])
         t0 = time.perf_counter()
         run(rows)
         t = time.perf_counter() - t0
-        if n >= B or t * 3 >= budget_s / 4:
+        if n >= B or t >= budget_s / 4:
             break
-        n = min(B, max(n + 1, int(n * max(2.0, (budget_s / 8) / max(t, 1e-3)))))
+        n = min(B, max(n + 1, int(n * min(8.0, max(2.0, (budget_s / 4) / max(t, 1e-3))))))
     reps = max(1, min(3, int(budget_s / max(t, 1e-3)) - 1))
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
         run(rows)
         times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    frac = len(rows) / B
-    return med, frac, cores, rows
+    del kc, vc, qc
+    return statistics.median(times), rows, cores
 
 
 def _measure_kv_write(steps, warmup):
@@ -268,13 +278,9 @@ def _measure_kv_write(steps, warmup):
             "algorithmic_bytes": nbytes}
 
 
-def _workload_metrics(w):
-    from sglang_restomod_amd import workloads
-
-    return workloads.algorithmic_bytes(w), workloads.algorithmic_flops(w)
-
-
-def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
+def _measure(index, steps, warmup, cpu_seconds, kv_format="e4m3"):
+    """Time workload ``index`` on the GPU (wall clock over ``steps`` calls, and HIP events
+    around every call on the launch stream), and its CPU baseline when ``cpu_seconds``."""
     import torch
 
     from sglang_restomod_amd import workloads
@@ -282,7 +288,7 @@ def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
     w = workloads.make(index, device=torch.device("cuda:0"), kv_format=kv_format)
     fn = _runner(w)
     wall_ms, per = _time_gpu(fn, steps, warmup)
-    nbytes, flops = _workload_metrics(w)
+    nbytes, flops = workloads.algorithmic_bytes(w), workloads.algorithmic_flops(w)
     ev_ms = statistics.mean(per)
     res = {
         "workload": w.name,
@@ -297,7 +303,7 @@ def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
         "TFLOPs": flops / (ev_ms * 1e-3) / 1e12,
         "wall_GBps": nbytes / (wall_ms * 1e-3) / 1e9,
         "wall_TFLOPs": flops / (wall_ms * 1e-3) / 1e12,
-        "tokens_per_s": (w.batch if w.mode == "decode" else int(w.extend_lens.sum())) / (wall_ms * 1e-3),
+        "tokens_per_s": int(w.extend_lens.sum()) / (wall_ms * 1e-3),
     }
     res["hbm_frac"] = res["GBps"] / HBM_PEAK_GBS
     res["mfma_frac"] = res["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
@@ -307,17 +313,69 @@ def _measure(index, steps, warmup, cpu_baseline, cpu_seconds, kv_format="e4m3"):
         tokens = 2 * int(sum(w.seq_lens_cpu))
         res["gather_ceiling_GBps"] = _gather_ceiling(tokens, w.heads_kv, row_bytes)
         res["gather_row_bytes"] = row_bytes
-    if cpu_baseline:
-        med, frac, cores, rows = _cpu_baseline(w, cpu_seconds)
-        sub_bytes = nbytes * frac if w.mode == "decode" else None
-        res["cpu"] = {
-            "seconds": med, "cores": cores, "sequences": len(rows), "of": w.batch,
-            "GBps": (nbytes * frac) / med / 1e9, "TFLOPs": (flops * frac) / med / 1e12,
-            "sample_bytes": sub_bytes,
-        }
+    if cpu_seconds:
+        sec, rows, cores = _cpu_baseline(w, cpu_seconds)
+        sb, sf = workloads.algorithmic_bytes(w, rows), workloads.algorithmic_flops(w, rows)
+        res["cpu"] = {"seconds": sec, "cores": cores, "sequences": len(rows), "of": w.batch,
+                      "GBps": sb / sec / 1e9, "TFLOPs": sf / sec / 1e12,
+                      "tokens_per_s": sum(w.extend_lens.tolist()[b] for b in rows) / sec}
     del w, fn
     torch.cuda.empty_cache()
     return res
+
+
+def _cpu_obj(r, bound_hbm):
+    c = r["cpu"]
+    return {
+        "value": round(c["GBps"] if bound_hbm else c["TFLOPs"], 5),
+        "unit": "GB/s" if bound_hbm else "TFLOP/s",
+        "cores": c["cores"],
+        "kind": "port",
+        "sample": (f"torch-native SDPA restatement (per-sequence gather + fp32 SDPA) over the {c['sequences']} "
+                   f"shortest of {c['of']} sequences, median of up to 3 passes of {c['seconds']:.3f} s; value = "
+                   f"algorithmic {'bytes' if bound_hbm else 'flops'} of those sequences per second"),
+    }
+
+
+def _roofline(r, kernel, bound_hbm):
+    achieved = r["GBps"] if bound_hbm else r["TFLOPs"]
+    peak = HBM_PEAK_GBS if bound_hbm else MFMA_BF16_PEAK_TFLOPS
+    obj = {
+        "bound": "hbm" if bound_hbm else "mfma",
+        "achieved": round(achieved, 3),
+        "peak": peak,
+        "unit": "GB/s" if bound_hbm else "TFLOP/s",
+        "frac": round(achieved / peak, 4),
+        "traffic": _traffic(kernel, r["workload"]),
+        "kernel_ms": round(r["event_ms_mean"], 5),
+        "timing": ("HIP events on the launch stream around each call (split-KV partial + merge)" if bound_hbm
+                   else "HIP events on the launch stream around each call (plan + extend kernel)"),
+    }
+    if bound_hbm:
+        ceil = r["gather_ceiling_GBps"]
+        obj["gather_ceiling"] = {
+            "GBps": round(ceil, 1), "frac": round(r["GBps"] / ceil, 4),
+            "pattern": f"the same K and V rows ({r['gather_row_bytes']} B per token and kv head) gathered from "
+                       "random pool slots by a plain load kernel, measured in this run"}
+    return obj
+
+
+def _family(r, kernel, bound_hbm):
+    """Compact object for a non-headline workload of the same JSON line."""
+    obj = {
+        "workload": r["workload"],
+        "kv_dtype": r["kv"],
+        "value": round(r["wall_GBps"] if bound_hbm else r["wall_TFLOPs"], 3),
+        "unit": "GB/s" if bound_hbm else "TFLOP/s",
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "tokens_per_s": round(r["tokens_per_s"], 1),
+        "roofline": _roofline(r, kernel, bound_hbm),
+    }
+    if r["mode"] == "verify":
+        obj["mfma_frac"] = round(r["mfma_frac"], 4)
+    if "cpu" in r:
+        obj["cpu_baseline"] = _cpu_obj(r, bound_hbm)
+    return obj
 
 
 def main():
@@ -335,8 +393,8 @@ def main():
     if args.calibrate_copy:
         _calibrate_copy(args.calibrate_copy)
         return
-    head = _measure(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_seconds,
-                    kv_format=args.kv_format)
+    cpu = 0 if args.no_cpu_baseline else args.cpu_seconds
+    head = _measure(args.workload, args.steps, args.warmup, cpu, kv_format=args.kv_format)
     bound_hbm = head["mode"] != "extend"
     kernel = "splitkv_partial" if bound_hbm else "extend_kernel"
     line = {
@@ -355,52 +413,28 @@ def main():
         "data": "synthetic (seeded N(0,1) q/k/v, shuffled token-pool slots)",
         "config": {"workload": head["workload"], "mode": head["mode"], "kv_dtype": head["kv"],
                    "tokens_per_s": round(head["tokens_per_s"], 1)},
-        "roofline": {
-            "bound": "hbm" if bound_hbm else "mfma",
-            "achieved": round(head["GBps"] if bound_hbm else head["TFLOPs"], 3),
-            "peak": HBM_PEAK_GBS if bound_hbm else MFMA_BF16_PEAK_TFLOPS,
-            "unit": "GB/s" if bound_hbm else "TFLOP/s",
-            "frac": round(head["hbm_frac"] if bound_hbm else head["mfma_frac"], 4),
-            "traffic": _traffic(kernel, head["workload"]),
-            "kernel_ms": round(head["event_ms_mean"], 5),
-            "timing": ("HIP events on the launch stream around each call (split-KV partial + merge)"
-                       if bound_hbm else "HIP events on the launch stream around each call"),
-        },
+        "roofline": _roofline(head, kernel, bound_hbm),
     }
-    if bound_hbm:
-        ceil = head["gather_ceiling_GBps"]
-        line["roofline"]["gather_ceiling"] = {
-            "GBps": round(ceil, 1),
-            "frac": round(head["GBps"] / ceil, 4),
-            "pattern": f"the same K and V rows ({head['gather_row_bytes']} B per token and kv head) gathered from "
-                       f"random pool slots by a plain load kernel, measured in this run",
-        }
     if "cpu" in head:
-        c = head["cpu"]
-        line["cpu_baseline"] = {
-            "value": round(c["GBps"] if bound_hbm else c["TFLOPs"], 4),
-            "unit": line["unit"],
-            "cores": c["cores"],
-            "kind": "port",
-            "sample": f"torch-native SDPA restatement (per-sequence gather + fp32 SDPA) over "
-                      f"{c['sequences']} of {c['of']} sequences, median of up to 3 after a sizing pass, "
-                      f"{c['seconds']:.3f} s per pass",
-        }
-    if args.secondary:
-        sec = {}
-        sec["kv_write"] = _measure_kv_write(max(10, args.steps // 2), args.warmup)
-        for idx, fmt in ((0, None), (2, None), (3, "e4m3"), (3, "e5m2"), (4, None)):
-            if idx == args.workload:
-                continue
-            try:
-                r = _measure(idx, max(10, args.steps // 2), args.warmup, False, 0, kv_format=fmt or "e4m3")
-            except NotImplementedError as exc:
-                sec[f"w{idx}"] = {"skipped": str(exc)}
-                continue
-            key = f"w{idx}" + (f"_{fmt}" if fmt else "")
-            sec[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()
-                        if k not in ("algorithmic_bytes", "algorithmic_flops")}
-        line["secondary"] = sec
+        line["cpu_baseline"] = _cpu_obj(head, bound_hbm)
+    if not args.headline_only:
+        # the other halves of the metric and the other configurations, each a compact object
+        steps = max(10, args.steps // 2)
+        sec_cpu = 0 if args.no_cpu_baseline else args.cpu_seconds_secondary
+        if args.workload != 2:
+            line["extend"] = _family(_measure(2, steps, args.warmup, sec_cpu), "extend_kernel", False)
+        fp8 = {}
+        for fmt in ("e4m3", "e5m2"):
+            fp8[fmt] = _family(_measure(3, steps, args.warmup, sec_cpu if fmt == "e4m3" else 0, kv_format=fmt),
+                               "splitkv_partial", True)
+        line["fp8_decode"] = fp8
+        if args.workload != 4:
+            line["verify"] = _family(_measure(4, steps, args.warmup, sec_cpu), "splitkv_partial", True)
+        if args.workload != 0:
+            r = _measure(0, steps, args.warmup, 0)
+            line["decode_b1"] = {"workload": r["workload"], "us_per_call": round(r["event_ms_mean"] * 1e3, 2),
+                                 "wall_us_per_call": round(r["ms_per_step"] * 1e3, 2)}
+        line["kv_write"] = _measure_kv_write(steps, args.warmup)
     print(json.dumps(line))
 
 

@@ -170,21 +170,26 @@ def kv_bytes_per_elem(w: Workload) -> int:
     return w.k_pool.element_size()
 
 
-def algorithmic_bytes(w: Workload) -> int:
-    """K+V read once per (token, kv head) + 4 B slot index per token + q in + out."""
-    tokens = sum(w.seq_lens_cpu)
+def algorithmic_bytes(w: Workload, rows=None) -> int:
+    """K+V read once per (token, kv head) + 4 B slot index per token + q in + out, over
+    every sequence or over the sequences ``rows``."""
+    rows = range(w.batch) if rows is None else rows
+    tokens = sum(w.seq_lens_cpu[b] for b in rows)
+    ext = w.extend_lens.tolist()
+    q_rows = sum(ext[b] for b in rows)
     kv = 2 * tokens * w.heads_kv * w.dim * kv_bytes_per_elem(w)
     idx = 4 * tokens
-    qo = 2 * w.q.numel() * w.q.element_size()
+    qo = 2 * q_rows * w.heads * w.dim * w.q.element_size()
     return kv + idx + qo
 
 
-def algorithmic_flops(w: Workload) -> int:
-    """4 * D * Hq * (visible query-key pairs)."""
+def algorithmic_flops(w: Workload, rows=None) -> int:
+    """4 * D * Hq * (visible query-key pairs), over every sequence or the sequences ``rows``."""
     pairs = 0
     ext = w.extend_lens.tolist()
     pre = w.prefix_lens.tolist()
-    for p, e in zip(pre, ext):
+    for b in (range(w.batch) if rows is None else rows):
+        p, e = pre[b], ext[b]
         # query i (0-based) sees p + i + 1 keys
         pairs += e * p + e * (e + 1) // 2
     return 4 * w.dim * w.heads * pairs
