@@ -292,6 +292,8 @@ def _measure(index, steps, warmup, cpu_seconds, kv_format="e4m3"):
     ev_ms = statistics.mean(per)
     res = {
         "workload": w.name,
+        # profiles/<kernel>__<this>.traffic.md: the name plus the fp8 format for fp8 pools
+        "profile_name": w.name + (f"_{w.kv_format}" if w.kv_format else ""),
         "mode": w.mode,
         "kv": str(w.k_pool.dtype).replace("torch.", ""),
         "ms_per_step": wall_ms,
@@ -346,7 +348,7 @@ def _roofline(r, kernel, bound_hbm):
         "peak": peak,
         "unit": "GB/s" if bound_hbm else "TFLOP/s",
         "frac": round(achieved / peak, 4),
-        "traffic": _traffic(kernel, r["workload"]),
+        "traffic": _traffic(kernel, r["profile_name"]),
         "kernel_ms": round(r["event_ms_mean"], 5),
         "timing": ("HIP events on the launch stream around each call (split-KV partial + merge)" if bound_hbm
                    else "HIP events on the launch stream around each call (plan + extend kernel)"),
