@@ -40,13 +40,14 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 8
+#define MA_ABI_VERSION 9
 
 /* dtype codes */
 #define MA_DT_F16 0
 #define MA_DT_BF16 1
 #define MA_DT_E4M3 2 /* OCP e4m3fn, stored as bytes */
 #define MA_DT_E5M2 3 /* OCP e5m2, stored as bytes */
+#define MA_DT_F32 4  /* output only: the attention result before its cast to 16 bits */
 
 /* status codes */
 #define MA_OK 0
@@ -94,7 +95,8 @@ size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim);
  *     segments that several waves shared.
  *   workspace: ma_splitkv_workspace_bytes(num_workgroups, head_dim) bytes, 256-byte
  *     aligned
- *   out [batch, num_q_heads, head_dim] in q_dtype
+ *   out [batch, num_q_heads, head_dim] in out_dtype: q_dtype, or MA_DT_F32 for the result
+ *     before its rounding to 16 bits (strides in elements of out_dtype)
  */
 int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
                       const void* k_cache, const void* v_cache, int64_t kv_stride_row,
@@ -103,7 +105,7 @@ int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
                       const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
                       int head_dim, int num_workgroups, float softmax_scale, float k_scale,
                       float v_scale, int sliding_window, void* workspace,
-                      size_t workspace_bytes, void* out, int64_t out_stride_tok,
+                      size_t workspace_bytes, void* out, int out_dtype, int64_t out_stride_tok,
                       int64_t out_stride_head, void* stream);
 
 /*
@@ -125,8 +127,8 @@ int ma_grouped_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_str
                               int64_t table_stride, const int64_t* row_index, int page_size,
                               const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
                               int head_dim, int num_workgroups, float softmax_scale, float k_scale,
-                              float v_scale, int sliding_window, void* out, int64_t out_stride_tok,
-                              int64_t out_stride_head, void* stream);
+                              float v_scale, int sliding_window, void* out, int out_dtype,
+                              int64_t out_stride_tok, int64_t out_stride_head, void* stream);
 
 /*
  * Grouped split-KV verify: a few query tokens per sequence (linear speculative
@@ -149,8 +151,8 @@ int ma_paged_verify(const void* q, int64_t q_stride_tok, int64_t q_stride_head, 
                     const int32_t* prefix_lens, int batch, int max_q_per_seq, int num_q_heads,
                     int num_kv_heads, int head_dim, int causal, int sliding_window,
                     int num_workgroups, float softmax_scale, float k_scale, float v_scale,
-                    void* workspace, size_t workspace_bytes, void* out, int64_t out_stride_tok,
-                    int64_t out_stride_head, void* stream);
+                    void* workspace, size_t workspace_bytes, void* out, int out_dtype,
+                    int64_t out_stride_tok, int64_t out_stride_head, void* stream);
 
 /*
  * Bytes of workspace ma_paged_extend needs for `num_tokens` query tokens in `batch`
@@ -178,7 +180,7 @@ size_t ma_extend_workspace_bytes(int64_t num_tokens, int num_q_heads, int num_kv
  *   workspace: ma_extend_workspace_bytes(num_tokens, ...) bytes, 256-byte aligned, no
  *   initialisation; calls that overlap in time must use different workspaces.
  *   The new tokens' K/V must already be in the pools.
- *   out [num_tokens, num_q_heads, head_dim] in q_dtype.
+ *   out [num_tokens, num_q_heads, head_dim] in out_dtype (q_dtype or MA_DT_F32).
  */
 int ma_paged_extend(const void* q, int64_t q_stride_tok, int64_t q_stride_head, int q_dtype,
                     int64_t num_tokens, const void* k_cache, const void* v_cache,
@@ -188,7 +190,8 @@ int ma_paged_extend(const void* q, int64_t q_stride_tok, int64_t q_stride_head, 
                     const int32_t* prefix_lens, int batch, int num_q_heads, int num_kv_heads,
                     int head_dim, int causal, int sliding_window, float softmax_scale,
                     float k_scale, float v_scale, void* workspace, size_t workspace_bytes,
-                    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream);
+                    void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
+                    void* stream);
 
 /*
  * KV write into the token pools with quantisation on write.

@@ -21,7 +21,7 @@ _LIB = None
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "libmi355x_attn.so")
 
-MA_DT_F16, MA_DT_BF16, MA_DT_E4M3, MA_DT_E5M2 = 0, 1, 2, 3
+MA_DT_F16, MA_DT_BF16, MA_DT_E4M3, MA_DT_E5M2, MA_DT_F32 = 0, 1, 2, 3, 4
 MA_OK = 0
 MA_EINVAL, MA_ELAUNCH, MA_EUNSUPPORTED = -1, -2, -3
 # grid limit of ma_grouped_decode_noalloc's static scratch (include/mi355x_attn.h)
@@ -41,7 +41,7 @@ SIGNATURES = {
         c_void_p, c_int, c_int, c_int, c_int,         # seq_lens, batch, hq, hkv, dim
         c_int, c_float, c_float, c_float,             # num_workgroups, scales
         c_int, c_void_p, c_size_t,                    # window, workspace, bytes
-        c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
+        c_void_p, c_int, c_int64, c_int64, c_void_p,  # out, out dtype, strides, stream
     ]),
     "ma_grouped_decode_noalloc": (c_int, [
         c_void_p, c_int64, c_int64, c_int,            # q, strides, dtype
@@ -49,7 +49,7 @@ SIGNATURES = {
         c_void_p, c_int64, c_void_p, c_int,           # table, stride, row_index, page size
         c_void_p, c_int, c_int, c_int, c_int,         # seq_lens, batch, hq, hkv, dim
         c_int, c_float, c_float, c_float, c_int,      # num_workgroups, scales, window
-        c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
+        c_void_p, c_int, c_int64, c_int64, c_void_p,  # out, out dtype, strides, stream
     ]),
     "ma_paged_verify": (c_int, [
         c_void_p, c_int64, c_int64, c_int, c_int64,   # q, strides, dtype, num_tokens
@@ -59,7 +59,7 @@ SIGNATURES = {
         c_int, c_int, c_int, c_int, c_int,            # batch, max_q, hq, hkv, dim
         c_int, c_int, c_int,                          # causal, window, num_workgroups
         c_float, c_float, c_float, c_void_p, c_size_t,  # scales, workspace, bytes
-        c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
+        c_void_p, c_int, c_int64, c_int64, c_void_p,  # out, out dtype, strides, stream
     ]),
     "ma_set_kv_buffer": (c_int, [
         c_void_p, c_void_p, c_int64, c_int64, c_int,  # k, v, strides, source dtype
@@ -93,7 +93,7 @@ SIGNATURES = {
         c_int, c_int, c_int, c_int,                   # batch, hq, hkv, dim
         c_int, c_int, c_float, c_float, c_float,      # causal, window, scales
         c_void_p, c_size_t,                           # workspace, bytes
-        c_void_p, c_int64, c_int64, c_void_p,         # out, strides, stream
+        c_void_p, c_int, c_int64, c_int64, c_void_p,  # out, out dtype, strides, stream
     ]),
 }
 

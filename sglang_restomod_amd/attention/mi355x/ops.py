@@ -179,6 +179,14 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+def _out_code(out: torch.Tensor, q: torch.Tensor) -> int:
+    """dtype code of an attention output: q's dtype, or float32 for the result before its
+    rounding to 16 bits."""
+    if out.shape != q.shape or out.dtype not in (q.dtype, torch.float32):
+        raise ValueError("out must have q's shape, and q's dtype or float32")
+    return _lib.MA_DT_F32 if out.dtype == torch.float32 else q_dtype_code(q.dtype)
+
+
 def grouped_decode_forward(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -197,7 +205,8 @@ def grouped_decode_forward(
     num_workgroups: Optional[int] = None,
     workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Decode one query token per sequence: ``q`` [B, Hq, D] -> [B, Hq, D] (q's dtype).
+    """Decode one query token per sequence: ``q`` [B, Hq, D] -> [B, Hq, D] in q's dtype, or
+    in float32 when ``out`` is float32 (the result before its rounding to 16 bits).
 
     ``page_table`` [rows, width] int32 maps (row, position // page_size) to a page;
     ``row_index`` [B] picks each sequence's row (None: row b). With page size 1
@@ -224,8 +233,7 @@ def grouped_decode_forward(
     table = _table(page_table)
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    if out.shape != q.shape or out.dtype != q.dtype:
-        raise ValueError("out must match q's shape and dtype")
+    out_code = _out_code(out, q)
     seq = _i32(seq_lens)
     ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
     del max_seq_len_hint  # the persistent grid does not depend on lengths
@@ -239,7 +247,7 @@ def grouped_decode_forward(
         seq.data_ptr(), B, Hq, Hkv, D,
         nwg, float(softmax_scale), float(k_scale), float(v_scale),
         int(sliding_window_size), _ptr(ws), nbytes,
-        out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
+        out.data_ptr(), out_code, out.stride(0), out.stride(1), _stream_ptr(dev),
     )
     _lib.check(status, "ma_grouped_decode")
     return out
@@ -290,8 +298,7 @@ def paged_verify_forward(
     B = seq_lens.shape[0]
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    if out.shape != q.shape or out.dtype != q.dtype:
-        raise ValueError("out must match q's shape and dtype")
+    out_code = _out_code(out, q)
     seq = _i32(seq_lens)
     qsl = _i32(query_start_loc)
     pre = None if prefix_kv_lens is None else _i32(prefix_kv_lens)
@@ -308,7 +315,7 @@ def paged_verify_forward(
         B, int(max_q_per_seq), Hq, Hkv, D,
         1 if causal else 0, int(sliding_window_size), nwg,
         float(softmax_scale), float(k_scale), float(v_scale), _ptr(ws), nbytes,
-        out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
+        out.data_ptr(), out_code, out.stride(0), out.stride(1), _stream_ptr(dev),
     )
     _lib.check(status, "ma_paged_verify")
     return out
@@ -421,8 +428,7 @@ def paged_extend_forward(
     table = _table(block_table)
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    if out.shape != q.shape or out.dtype != q.dtype:
-        raise ValueError("out must match q's shape and dtype")
+    out_code = _out_code(out, q)
     B = seq_lens.shape[0]
     seq = _i32(seq_lens)
     qsl = _i32(query_start_loc)
@@ -443,7 +449,7 @@ def paged_extend_forward(
         seq.data_ptr(), qsl.data_ptr(), _ptr(pre),
         B, Hq, Hkv, D, 1 if causal else 0, int(sliding_window_size),
         float(softmax_scale), float(k_scale), float(v_scale), _ptr(ws), nbytes,
-        out.data_ptr(), out.stride(0), out.stride(1), _stream_ptr(dev),
+        out.data_ptr(), out_code, out.stride(0), out.stride(1), _stream_ptr(dev),
     )
     _lib.check(status, "ma_paged_extend")
     return out

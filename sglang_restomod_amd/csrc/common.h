@@ -61,7 +61,7 @@ __device__ __forceinline__ const T MA_CONST* cptr(const T* p) {
 #endif
 
 // dtype codes shared with the C ABI (include/mi355x_attn.h)
-enum DType : int { DT_F16 = 0, DT_BF16 = 1, DT_E4M3 = 2, DT_E5M2 = 3 };
+enum DType : int { DT_F16 = 0, DT_BF16 = 1, DT_E4M3 = 2, DT_E5M2 = 3, DT_F32 = 4 };
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kEmptyLse = -1073741824.0f;  // -2^30: LSE of a split that saw no key
@@ -219,6 +219,20 @@ __device__ __forceinline__ uint16_t f2h(float x) {
     return (uint16_t)(u >> 16);
   } else {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+}
+
+// Four consecutive output values of one row, scaled by s, at element `off` of out: fp32
+// when out_f32 (the kernels' pre-cast result, for checking), else the query's 16-bit dtype.
+template <bool BF16>
+__device__ __forceinline__ void store_out4(void* out, int64_t off, f32x4 v, float s, bool out_f32) {
+  if (out_f32) {
+    *reinterpret_cast<f32x4 MA_GLOBAL*>(gptr_mut(reinterpret_cast<float*>(out)) + off) = v * s;
+  } else {
+    u32x2 w;
+    w[0] = (uint32_t)f2h<BF16>(v[0] * s) | ((uint32_t)f2h<BF16>(v[1] * s) << 16);
+    w[1] = (uint32_t)f2h<BF16>(v[2] * s) | ((uint32_t)f2h<BF16>(v[3] * s) << 16);
+    *reinterpret_cast<u32x2 MA_GLOBAL*>(gptr_mut(reinterpret_cast<uint16_t*>(out)) + off) = w;
   }
 }
 

@@ -90,7 +90,8 @@ struct ExtendArgs {
   float scale_log2;
   float v_scale;
   void* out;
-  int64_t out_stride_tok, out_stride_head;
+  int64_t out_stride_tok, out_stride_head;  // elements of the output dtype
+  int out_f32;                              // out holds fp32 (else the query dtype)
 };
 
 // Keys [lo, hi) that some row of the bm-row tile starting at row r0 of a sequence may see.
@@ -633,15 +634,9 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     const int t = r / a.group;
     const int g = r - t * a.group;
     const float inv = (lt > 0.f) ? a.v_scale / lt : 0.f;
-    uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) + (int64_t)(tok0 + t) * a.out_stride_tok +
-                             (int64_t)(h * a.group + g) * a.out_stride_head;
+    const int64_t off = (int64_t)(tok0 + t) * a.out_stride_tok + (int64_t)(h * a.group + g) * a.out_stride_head;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      u32x2 w;
-      w[0] = (uint32_t)f2h<QBF16>(o[rb][db][0] * inv) | ((uint32_t)f2h<QBF16>(o[rb][db][1] * inv) << 16);
-      w[1] = (uint32_t)f2h<QBF16>(o[rb][db][2] * inv) | ((uint32_t)f2h<QBF16>(o[rb][db][3] * inv) << 16);
-      *reinterpret_cast<u32x2 MA_GLOBAL*>(op + db * 16 + 4 * j) = w;
-    }
+    for (int db = 0; db < DB; ++db) store_out4<QBF16>(a.out, off + db * 16 + 4 * j, o[rb][db], inv, a.out_f32);
   }
 }
 
@@ -689,14 +684,15 @@ extern "C" int ma_paged_extend(
     const int32_t* seq_lens, const int32_t* query_start_loc, const int32_t* prefix_lens,
     int batch, int num_q_heads, int num_kv_heads, int head_dim,
     int causal, int sliding_window, float softmax_scale, float k_scale, float v_scale,
-    void* workspace, size_t workspace_bytes, void* out, int64_t out_stride_tok, int64_t out_stride_head,
-    void* stream) {
+    void* workspace, size_t workspace_bytes, void* out, int out_dtype, int64_t out_stride_tok,
+    int64_t out_stride_head, void* stream) {
   const int bm = extend_tile_rows(head_dim);
   if (bm == 0) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (64, 128 or 256)", head_dim);
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
   if (kv_dtype < 0 || kv_dtype > DT_E5M2) return set_error(MA_EINVAL, "kv dtype %d unknown", kv_dtype);
   if ((kv_dtype == DT_F16 || kv_dtype == DT_BF16) && kv_dtype != q_dtype)
     return set_error(MA_EINVAL, "16-bit KV dtype must equal the query dtype");
+  if (out_dtype != q_dtype && out_dtype != DT_F32) return set_error(MA_EINVAL, "out dtype %d must be the query dtype or f32", out_dtype);
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads)
     return set_error(MA_EINVAL, "bad head counts hq=%d hkv=%d", num_q_heads, num_kv_heads);
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
@@ -712,8 +708,10 @@ extern "C" int ma_paged_extend(
   const int elt = (kv_dtype >= DT_E4M3) ? 1 : 2;
   if (kv_stride_row * elt >= ((int64_t)1 << 32))
     return set_error(MA_EUNSUPPORTED, "KV row stride of %lld bytes exceeds 4 GiB", (long long)(kv_stride_row * elt));
+  const int out_elt = out_dtype == DT_F32 ? 4 : 2;
+  const int out_align = out_dtype == DT_F32 ? 15 : 7;  // f32x4 or 4 x 16-bit stores
   if (((kv_stride_row * elt) & 15) || ((kv_stride_head * elt) & 15) || ((q_stride_tok * 2) & 15) ||
-      ((q_stride_head * 2) & 15) || ((out_stride_tok * 2) & 7) || ((out_stride_head * 2) & 7))
+      ((q_stride_head * 2) & 15) || ((out_stride_tok * out_elt) & out_align) || ((out_stride_head * out_elt) & out_align))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   const int group = num_q_heads / num_kv_heads;
   const int64_t items = extend_items(num_tokens, group, batch, bm);
@@ -743,6 +741,7 @@ extern "C" int ma_paged_extend(
   a.causal = p.causal; a.window = p.window;
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
+  a.out_f32 = out_dtype == DT_F32;
   const dim3 grid((unsigned)(items * num_kv_heads));
   const bool qbf16 = q_dtype == DT_BF16;
   e = head_dim == 64    ? launch_extend_d<64>(qbf16, kv_dtype, grid, (hipStream_t)stream, a)

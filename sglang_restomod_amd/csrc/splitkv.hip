@@ -95,7 +95,8 @@ struct SplitKVArgs {
   float* part_o;             // [nwaves][2][kMaxRows][D]
   float* part_lse;           // [nwaves][2][kMaxRows]
   void* out;
-  int64_t out_stride_tok, out_stride_head;
+  int64_t out_stride_tok, out_stride_head;  // elements of the output dtype
+  int out_f32;                              // out holds fp32 (else the query dtype)
 };
 
 // Geometry of one sequence.
@@ -199,9 +200,8 @@ __device__ __forceinline__ void write_zero_rows(const SplitKVArgs& a, int b) {
     const int d4 = (idx - row * (D / 4)) * 4;
     const int t = row / a.hq;
     const int h = row - t * a.hq;
-    uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) + (int64_t)(g.tok0 + t) * a.out_stride_tok +
-                             (int64_t)h * a.out_stride_head + d4;
-    *reinterpret_cast<u32x2 MA_GLOBAL*>(op) = u32x2{0u, 0u};
+    const int64_t off = (int64_t)(g.tok0 + t) * a.out_stride_tok + (int64_t)h * a.out_stride_head + d4;
+    store_out4<false>(a.out, off, f32x4{0.f, 0.f, 0.f, 0.f}, 0.f, a.out_f32);
   }
 }
 
@@ -279,14 +279,6 @@ __device__ __forceinline__ void cursor_next(const SplitKVArgs& a, Cursor& c, int
     ++b;
     c.g = geom_u<TS>(a, b);
   } while (c.g.nt == 0 || c.g.rg_real == 0);
-}
-
-template <bool BF16>
-__device__ __forceinline__ u32x2 pack4(f32x4 v, float s) {
-  u32x2 pk;
-  pk[0] = (uint32_t)f2h<BF16>(v[0] * s) | ((uint32_t)f2h<BF16>(v[1] * s) << 16);
-  pk[1] = (uint32_t)f2h<BF16>(v[2] * s) | ((uint32_t)f2h<BF16>(v[3] * s) << 16);
-  return pk;
 }
 
 // Wave index holding global tile t in a grid of nw waves over `total` tiles.
@@ -540,12 +532,10 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       const int g = R - t * a.group;
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
       if (whole) {
-        uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) + (int64_t)(cu.g.tok0 + t) * a.out_stride_tok +
-                                 (int64_t)(cu.h * a.group + g) * a.out_stride_head;
+        const int64_t off = (int64_t)(cu.g.tok0 + t) * a.out_stride_tok + (int64_t)(cu.h * a.group + g) * a.out_stride_head;
         const float sc = inv * a.v_scale;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-          *reinterpret_cast<u32x2 MA_GLOBAL*>(op + db * 16 + 4 * j) = pack4<QBF16>(o[nb][db], sc);
+        for (int db = 0; db < DB; ++db) store_out4<QBF16>(a.out, off + db * 16 + 4 * j, o[nb][db], sc, a.out_f32);
       } else {
         const int64_t pidx = ((int64_t)W * 2 + slot_sel) * kMaxRows + nb * 16 + c;
         float MA_GLOBAL* po = gptr_mut(a.part_o) + pidx * D;
@@ -897,10 +887,8 @@ __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
       const int t = R / a.group;
       const int gg = R - t * a.group;
       if (row >= kRows || t >= g.ntok) continue;
-      uint16_t MA_GLOBAL* op = gptr_mut(reinterpret_cast<uint16_t*>(a.out)) +
-                               (int64_t)(g.tok0 + t) * a.out_stride_tok +
-                               (int64_t)(h * a.group + gg) * a.out_stride_head + d4;
-      *reinterpret_cast<u32x2 MA_GLOBAL*>(op) = pack4<QBF16>(acc[i], a.v_scale / wsum[i]);
+      const int64_t off = (int64_t)(g.tok0 + t) * a.out_stride_tok + (int64_t)(h * a.group + gg) * a.out_stride_head + d4;
+      store_out4<QBF16>(a.out, off, acc[i], a.v_scale / wsum[i], a.out_f32);
     }
   }
 }
@@ -1038,8 +1026,11 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
        reinterpret_cast<uintptr_t>(a.out)) & 15)
     return set_error(MA_EINVAL, "q, k, v and out must be 16-byte aligned");
   const int elt = (kv_dtype >= DT_E4M3) ? 1 : 2;
+  const int out_elt = a.out_f32 ? 4 : 2;
+  const int out_align = a.out_f32 ? 15 : 7;  // f32x4 or 4 x 16-bit stores
   if (((a.kv_stride_row * elt) & 15) || ((a.kv_stride_head * elt) & 15) || ((a.q_stride_tok * 2) & 15) ||
-      ((a.q_stride_head * 2) & 15) || ((a.out_stride_tok * 2) & 7) || ((a.out_stride_head * 2) & 7))
+      ((a.q_stride_head * 2) & 15) || ((a.out_stride_tok * out_elt) & out_align) ||
+      ((a.out_stride_head * out_elt) & out_align))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   a.group = a.hq / a.hkv;
   if ((int64_t)a.num_tokens * a.group > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens x GQA group exceeds 2^31");
@@ -1078,8 +1069,10 @@ extern "C" int ma_grouped_decode(
     const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
     int num_workgroups, float softmax_scale, float k_scale, float v_scale,
     int sliding_window, void* workspace, size_t workspace_bytes,
-    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+    void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
+  if ((q_dtype == DT_F16 || q_dtype == DT_BF16) && out_dtype != q_dtype && out_dtype != DT_F32)
+    return set_error(MA_EINVAL, "out dtype %d must be the query dtype or f32", out_dtype);
   SplitKVArgs a{};
   a.q = q; a.q_stride_tok = q_stride_tok; a.q_stride_head = q_stride_head;
   a.k = k_cache; a.v = v_cache; a.kv_stride_row = kv_stride_row; a.kv_stride_head = kv_stride_head;
@@ -1090,6 +1083,7 @@ extern "C" int ma_grouped_decode(
   a.causal = 1; a.window = sliding_window < 0 ? -1 : sliding_window;
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
+  a.out_f32 = out_dtype == DT_F32;
   return splitkv_run(a, head_dim, q_dtype, kv_dtype, 1, num_workgroups, workspace, workspace_bytes,
                      (hipStream_t)stream);
 }
@@ -1102,7 +1096,9 @@ extern "C" int ma_paged_verify(
     int batch, int max_q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
     int causal, int sliding_window, int num_workgroups,
     float softmax_scale, float k_scale, float v_scale, void* workspace, size_t workspace_bytes,
-    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+    void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+  if ((q_dtype == DT_F16 || q_dtype == DT_BF16) && out_dtype != q_dtype && out_dtype != DT_F32)
+    return set_error(MA_EINVAL, "out dtype %d must be the query dtype or f32", out_dtype);
   if (num_tokens < 0 || num_tokens > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens %lld out of range", (long long)num_tokens);
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
   if (!query_start_loc) return set_error(MA_EINVAL, "query_start_loc is required");
@@ -1117,6 +1113,7 @@ extern "C" int ma_paged_verify(
   a.causal = causal ? 1 : 0; a.window = sliding_window < 0 ? -1 : sliding_window;
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
+  a.out_f32 = out_dtype == DT_F32;
   return splitkv_run(a, head_dim, q_dtype, kv_dtype, max_q_per_seq, num_workgroups, workspace, workspace_bytes,
                      (hipStream_t)stream);
 }
@@ -1127,7 +1124,7 @@ extern "C" int ma_grouped_decode_noalloc(
     const int32_t* table, int64_t table_stride, const int64_t* row_index, int page_size,
     const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
     int num_workgroups, float softmax_scale, float k_scale, float v_scale, int sliding_window,
-    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+    void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
   if (num_workgroups <= 0 || num_workgroups > kScratchWorkgroups)
     return set_error(MA_EINVAL, "num_workgroups %d: the static scratch serves 1..%d", num_workgroups, kScratchWorkgroups);
   if (head_dim > 256) return set_error(MA_EUNSUPPORTED, "head_dim %d exceeds the static scratch's 256", head_dim);
@@ -1137,5 +1134,5 @@ extern "C" int ma_grouped_decode_noalloc(
   return ma_grouped_decode(q, q_stride_tok, q_stride_head, q_dtype, k_cache, v_cache, kv_stride_row, kv_stride_head,
                            kv_dtype, table, table_stride, row_index, page_size, seq_lens, batch, num_q_heads,
                            num_kv_heads, head_dim, num_workgroups, softmax_scale, k_scale, v_scale, sliding_window, ws,
-                           kScratchBytes, out, out_stride_tok, out_stride_head, stream);
+                           kScratchBytes, out, out_dtype, out_stride_tok, out_stride_head, stream);
 }

@@ -55,7 +55,7 @@ def _decode_args(**over):
     args = dict(q=1 << 20, qs0=1024, qs1=128, qdt=1, k=1 << 21, v=1 << 22, rs=1024, hs=128, kvdt=1,
                 table=1 << 23, tstride=64, rowidx=None, ps=1, seq=1 << 24, batch=2, hq=8, hkv=8, dim=128,
                 nwg=4, sm=0.1, ks=1.0, vs=1.0, win=-1, ws=None, wsb=0,
-                out=1 << 25, os0=1024, os1=128, stream=None)
+                out=1 << 25, odt=1, os0=1024, os1=128, stream=None)
     args.update(over)
     return list(args.values())
 
@@ -71,6 +71,8 @@ def _decode_args(**over):
     ({"ws": None, "wsb": 0}, "workspace"),
     ({"ws": 1 << 26, "wsb": 1024}, "workspace too small"),
     ({"nwg": 0}, "num_workgroups"),
+    ({"odt": 2}, "out dtype"),
+    ({"odt": 4, "os1": 130}, "aligned"),
 ])
 def test_bad_arguments_are_rejected_before_launch(lib, over, msg):
     status = lib.ma_grouped_decode(*_decode_args(**over))
@@ -119,7 +121,7 @@ def _extend_args(**over):
     args = dict(q=1 << 20, qs0=1024, qs1=128, qdt=1, T=64, k=1 << 21, v=1 << 22, rs=1024, hs=128, kvdt=1,
                 table=1 << 23, tstride=64, rowidx=None, ps=1, seq=1 << 24, qsl=1 << 25, pre=None,
                 batch=2, hq=16, hkv=2, dim=128, causal=1, win=-1, sm=0.1, ks=1.0, vs=1.0,
-                ws=1 << 26, wsb=1 << 12, out=1 << 27, os0=1024, os1=128, stream=None)
+                ws=1 << 26, wsb=1 << 12, out=1 << 27, odt=1, os0=1024, os1=128, stream=None)
     args.update(over)
     return list(args.values())
 
@@ -137,6 +139,8 @@ def _extend_args(**over):
     ({"ws": None}, "workspace too small"),
     ({"wsb": 8}, "workspace too small"),
     ({"ws": (1 << 26) + 64}, "256-byte aligned"),
+    ({"odt": 0}, "out dtype"),
+    ({"odt": 4, "os0": 1026}, "aligned"),
 ])
 def test_extend_rejects_bad_arguments(lib, over, msg):
     assert lib.ma_paged_extend(*_extend_args(**over)) != 0

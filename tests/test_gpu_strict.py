@@ -1,0 +1,82 @@
+"""Every output of every benchmark workload, at full size, against the float64 closed form
+(oracle.torch_f64, evaluated on the GPU that holds the inputs) to the stated bound:
+
+* the kernels' fp32 output (the result before its rounding to 16 bits): max |err| <= 2e-3
+  on the softmax-normalised output, with no other allowance;
+* the 16-bit output: |err| <= 2e-3 + half an ulp of the reference value in that dtype
+  (an exact result rounded to bf16 is already up to half an ulp away).
+
+Workloads: decode B=1 (fp16), decode B=64 (bf16), fp8 decode B=128 in e4m3 and e5m2,
+verify B=32 x 4, extend B=8 (every row), and the head-dim-256 decode and extend.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import torch_f64 as F64
+from sglang_restomod_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+ATOL = 2e-3
+
+
+def _ops():
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    return ops
+
+
+def _call(w, out):
+    ops = _ops()
+    if w.mode == "decode":
+        return ops.grouped_decode_forward(w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens,
+                                          softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale,
+                                          out=out, row_index=w.req_pool_indices)
+    qsl = w.query_start_loc
+    if w.mode == "verify":
+        return ops.paged_verify_forward(w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens,
+                                        max_q_per_seq=int(w.extend_lens.max()), softmax_scale=w.softmax_scale,
+                                        k_scale=w.k_scale, v_scale=w.v_scale, out=out,
+                                        row_index=w.req_pool_indices)
+    return ops.paged_extend_forward(w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens,
+                                    softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale,
+                                    out=out, row_index=w.req_pool_indices)
+
+
+def _half_ulp(ref: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    mant = 7 if dtype == torch.bfloat16 else 10
+    mag = ref.abs().clamp_min(2.0 ** -14)
+    return 0.5 * torch.exp2(torch.floor(torch.log2(mag)) - mant)
+
+
+CASES = [(0, "e4m3"), (1, "e4m3"), (3, "e4m3"), (3, "e5m2"), (4, "e4m3"), (2, "e4m3"), (5, "e4m3"), (6, "e4m3")]
+
+
+@pytest.mark.parametrize("index,fmt", CASES)
+def test_every_output_at_full_size(index, fmt):
+    w = workloads.make(index, device=DEV, kv_format=fmt)
+    tag = w.name + (f"_{fmt}" if w.kv_format else "")
+    print(f"[case] strict {tag}: {w.batch} sequences, {w.q.shape[0]} query rows", flush=True)
+    slots = F64.rows_of_table(w.req_to_token, w.req_pool_indices, w.seq_lens_cpu)
+    ref = F64.attend(w.q, w.k_pool, w.v_pool, slots, w.query_start_loc.tolist(), w.prefix_lens.tolist(),
+                     w.seq_lens_cpu, softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale)
+    out32 = _call(w, torch.empty(w.q.shape, dtype=torch.float32, device=DEV))
+    out16 = _call(w, torch.empty_like(w.q))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out32).all() and torch.isfinite(out16).all()
+    err32 = (out32.double() - ref).abs()
+    err16 = (out16.double() - ref).abs()
+    bound16 = ATOL + _half_ulp(ref, w.q.dtype)
+    worst32 = float(err32.max())
+    print(f"[result] {tag}: max |err| fp32 out {worst32:.3e}, 16-bit out {float(err16.max()):.3e}, "
+          f"16-bit excess over its bound {float((err16 - bound16).max()):.3e}", flush=True)
+    assert worst32 <= ATOL, f"{tag}: fp32 output off by {worst32:.3e}"
+    assert bool((err16 <= bound16).all()), f"{tag}: 16-bit output beyond 2e-3 + half an ulp"
+    # the 16-bit output is the fp32 one rounded to 16 bits: at most one ulp apart (the
+    # compiler may fuse the final scaling into a single rounding to 16 bits)
+    gap = (out16.double() - out32.double()).abs()
+    assert bool((gap <= 2 * _half_ulp(out32.double(), w.q.dtype)).all()), f"{tag}: 16-bit output is not the fp32 result rounded"

@@ -186,3 +186,42 @@ def test_flop_and_byte_counts_are_closed_form():
     assert workloads.algorithmic_flops(w) == 4 * w.dim * w.heads * pairs
     d = workloads.make(0)
     assert workloads.algorithmic_bytes(d) == 2 * 512 * 8 * 128 * 2 + 4 * 512 + 2 * 32 * 128 * 2
+
+
+@pytest.mark.parametrize("index,fmt", [(0, None), (1, None), (2, None), (4, None), (3, "e4m3"), (3, "e5m2"),
+                                       (5, None), (6, None)])
+def test_float64_torch_form_matches_the_oracle(index, fmt):
+    """oracle.torch_f64 (the full-size reference of the GPU tests) against the numpy oracle
+    on every workload's shape, shrunk: identical to float64 rounding."""
+    from oracle import torch_f64 as F64
+
+    w = workloads.make(index, batch=3, scale_lens=0.03, kv_format=fmt or "e4m3")
+    kf = w.k_pool.double().numpy()
+    vf = w.v_pool.double().numpy()
+    r2t, rpi = w.req_to_token.numpy(), w.req_pool_indices.numpy()
+    common = dict(softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale)
+    if w.mode == "decode":
+        ref = A.decode(w.q.double().numpy(), kf, vf, r2t, rpi, w.seq_lens.numpy(), **common)
+    else:
+        ref = A.extend(w.q.double().numpy(), kf, vf, r2t, rpi, w.prefix_lens.numpy(), w.extend_lens.numpy(),
+                       **common)
+    slots = F64.rows_of_table(w.req_to_token, w.req_pool_indices, w.seq_lens_cpu)
+    got = F64.attend(w.q, w.k_pool, w.v_pool, slots, w.query_start_loc.tolist(), w.prefix_lens.tolist(),
+                     w.seq_lens_cpu, **common)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("window,causal", [(5, True), (0, True), (7, False)])
+def test_float64_torch_form_windows_and_masks(window, causal):
+    from oracle import torch_f64 as F64
+
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(9, 4, 16, generator=g, dtype=torch.float64)
+    k = torch.randn(40, 2, 16, generator=g, dtype=torch.float64)
+    v = torch.randn(40, 2, 16, generator=g, dtype=torch.float64)
+    slots = [torch.randperm(40, generator=g)[:30], torch.randperm(40, generator=g)[:12]]
+    qsl, pre, seq = [0, 6, 9], [24, 9], [30, 12]
+    ref = A.paged_attention(q.numpy(), k.numpy(), v.numpy(), [s.numpy() for s in slots], qsl, pre, seq,
+                            softmax_scale=0.3, causal=causal, sliding_window=window)
+    got = F64.attend(q, k, v, slots, qsl, pre, seq, softmax_scale=0.3, causal=causal, sliding_window=window)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=0, atol=1e-12)
