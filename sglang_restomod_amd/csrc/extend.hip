@@ -323,6 +323,13 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     for (int kk = 0; kk < KK; ++kk)
       qv[rb][kk] = real[rb] ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + kk * 8) : u32x4{0, 0, 0, 0};
   }
+  // Q is waited for here, once. The compiler cannot count the loads issued by inline
+  // assembly below, so a Q load still outstanding at the first score MFMA in the loop
+  // is waited for with vmcnt(0), which drains every K/V tile in flight, once per pass.
+#pragma unroll
+  for (int rb = 0; rb < kXRB; ++rb)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) __asm__ volatile("" : "+v"(qv[rb][kk]));
   // keys any row of the workgroup may see, and the window in which no row needs masking
   const int t_first = r0 / a.group;
   const int t_last = min(ntok - 1, (r0 + kXBM - 1) / a.group);
