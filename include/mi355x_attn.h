@@ -26,9 +26,12 @@
  * (sglang_restomod/attention/v100/tilelang/_paged_adapter.py:658,753-754).
  * Query head h reads kv head h / (num_q_heads / num_kv_heads).
  *
- * Head dims of the attention entry points: 64, 128 or 256, with every KV dtype (the
- * reference's paged kernels have configurations for 64, 128, 256 and 512,
- * _kernels_paged.py:398-410). Other head dims return MA_EUNSUPPORTED.
+ * Head dims of the attention entry points: every multiple of 16 from 16 to 512, with
+ * every KV dtype (the reference's paged kernels take any head dim: configurations for
+ * 64, 128, 256 and 512 and a default for the rest, _kernels_paged.py:397-418). 64, 128
+ * and 256 run on the split-KV and tiled extend kernels; the others on one kernel that
+ * serves decode, verify and extend rows alike (16 rows per wave, no split over keys, no
+ * workspace). Other head dims return MA_EUNSUPPORTED.
  */
 #ifndef MI355X_ATTN_H
 #define MI355X_ATTN_H
@@ -74,7 +77,8 @@ int ma_device_workgroups(void);
  * Bytes of workspace the split-KV entry points need for a persistent grid of
  * `num_workgroups` workgroups (1..16384): one descriptor per wave, then the partial
  * results of segments shared by several waves. No initialisation is needed; calls
- * that overlap in time must use different workspaces.
+ * that overlap in time must use different workspaces. 0 at the head dims other than
+ * 64, 128 and 256, whose kernel needs none.
  */
 size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim);
 
@@ -115,7 +119,8 @@ int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
  * Same arguments and results as ma_grouped_decode minus the workspace: the split-KV
  * partials go to a static scratch array in the library's device code (one copy per GPU,
  * held from the library's first use on that GPU until the process ends) sized for
- * num_workgroups <= MA_NOALLOC_MAX_WORKGROUPS at head_dim <= 256: 67,403,776 bytes.
+ * num_workgroups <= MA_NOALLOC_MAX_WORKGROUPS at head_dim <= 256: 67,403,776 bytes (the
+ * head dims other than 64, 128 and 256 run on a kernel that uses no scratch).
  * Larger grids return MA_EINVAL. Nothing is allocated or freed; the scratch needs no
  * clearing (every call rewrites what it reads). Calls that overlap in time on one GPU
  * (two streams) share the scratch and race: serialise them.

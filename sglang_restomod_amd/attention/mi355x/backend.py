@@ -11,8 +11,8 @@ What differs by design:
 
 * Every supported layer runs on the HIP kernels: decode, prefix-aware extend,
   linear target verify and draft extend. Nothing is delegated to another backend,
-  and layers the kernels cannot serve (head_dim other than 64, 128 or 256, logit
-  soft-capping, attention sinks, cross-attention, tree-shaped verify) raise
+  and layers the kernels cannot serve (a head dim that is not a multiple of 16 up to
+  512, logit soft-capping, attention sinks, cross-attention, tree-shaped verify) raise
   ``NotImplementedError`` naming the reason, instead of running elsewhere.
 * The kernels address SGLang's ``req_to_token`` directly (page size 1,
   ``req_pool_indices`` as the row index), so the metadata is the engine's own
@@ -109,10 +109,10 @@ class MI355XAttnBackend(_EngineBase):
         self.kv_cache_dtype = getattr(model_runner, "kv_cache_dtype", None)
         head_dim = int(model_runner.model_config.head_dim)
         v_head_dim = int(getattr(model_runner.model_config, "v_head_dim", head_dim))
-        if head_dim != v_head_dim or head_dim not in ops.SUPPORTED_HEAD_DIMS:
+        if head_dim != v_head_dim or not ops.head_dim_supported(head_dim):
             raise NotImplementedError(
-                f"mi355x_attn serves head_dim {ops.SUPPORTED_HEAD_DIMS} with equal q/k and v dims "
-                f"(model has qk {head_dim}, v {v_head_dim})")
+                f"mi355x_attn serves a head_dim that is a multiple of {ops.HEAD_DIM_MULTIPLE} up to "
+                f"{ops.MAX_HEAD_DIM} with equal q/k and v dims (model has qk {head_dim}, v {v_head_dim})")
         if self.req_to_token.dtype != torch.int32:
             raise ValueError("req_to_token must be int32")
         self.head_dim = head_dim

@@ -230,7 +230,9 @@ class MI355XMultiStepDraftBackend:
         self.swa_mapping = getattr(self.token_to_kv_pool, "full_to_swa_index_mapping", None)
         self.native_kv_write = env_flag(ENV_NATIVE_KV_WRITE, "1")
         model_config = getattr(model_runner, "model_config", None)
-        self.head_dim = int(getattr(model_config, "head_dim", max(plan.SUPPORTED_HEAD_DIMS)))
+        # the model's head dim sizes the workspace made before capture; without one, the
+        # head dim with the largest split-KV workspace
+        self.head_dim = int(getattr(model_config, "head_dim", max(ops.TUNED_HEAD_DIMS)))
         self.max_context_len = int(getattr(model_config, "context_len", self.req_to_token.shape[1]))
         self.passes = self.speculative_num_steps - 1
         self.attn_backends = [MI355XDraftDecodeBackend(self, i) for i in range(self.passes)]
@@ -239,18 +241,18 @@ class MI355XMultiStepDraftBackend:
             obj.decode_attention_backend_str = stamp
         self.current: Optional[DraftRows] = None
         self._ws: Optional[torch.Tensor] = None
-        self._ws_dim = 0
         self._graph: Optional[dict] = None
 
     # ---- buffers ----
     def workspace(self, head_dim: int) -> torch.Tensor:
         """One split-KV workspace for every pass (the passes run one after another on the
         engine's stream), grown for a wider layer outside graph capture only."""
-        if self._ws is None or self._ws_dim < head_dim:
+        need = ops.splitkv_workspace_bytes(self.device, head_dim)
+        if self._ws is None or self._ws.numel() < need:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError("the draft workspace must exist before graph capture (init_cuda_graph_state)")
-            self._ws = ops.splitkv_workspace(self.device, head_dim=max(head_dim, self.head_dim))
-            self._ws_dim = max(head_dim, self.head_dim)
+            widest = max((head_dim, self.head_dim), key=lambda d: ops.splitkv_workspace_bytes(self.device, d))
+            self._ws = ops.splitkv_workspace(self.device, head_dim=widest)
         return self._ws
 
     def _needs_table(self) -> bool:

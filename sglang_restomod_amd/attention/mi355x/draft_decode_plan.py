@@ -12,7 +12,8 @@ from __future__ import annotations
 
 import torch
 
-SUPPORTED_HEAD_DIMS = (64, 128, 256)  # the kernels' head dims (ops.SUPPORTED_HEAD_DIMS)
+PAGE_SIZE = 16        # head dims are multiples of this (draft_decode_plan.py:22, :93-94)
+MAX_HEAD_DIM = 512    # the widest head dim the kernels take (ops.MAX_HEAD_DIM)
 
 
 def page_table_from_indices(
@@ -59,8 +60,10 @@ def layer_shape_reason(layer) -> str | None:
         return f"gqa_ratio(h={hq},hkv={hkv})"
     if qk != vd:
         return f"qk_dim({qk})!=v_dim({vd})"
-    if qk not in SUPPORTED_HEAD_DIMS:
-        return f"head_dim({qk})_not_in_{SUPPORTED_HEAD_DIMS}"
+    if qk % PAGE_SIZE:
+        return f"dim({qk})_not_a_multiple_of_{PAGE_SIZE}"
+    if qk <= 0 or qk > MAX_HEAD_DIM:
+        return f"head_dim({qk})_not_in_1..{MAX_HEAD_DIM}"
     if getattr(layer, "is_cross_attention", False):
         return "cross_attention"
     if getattr(layer, "logit_cap", None) not in (None, 0, 0.0):

@@ -27,7 +27,16 @@ from . import _lib
 FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 
 VERIFY_MAX_Q_PER_SEQ = 64
-SUPPORTED_HEAD_DIMS = (64, 128, 256)
+TUNED_HEAD_DIMS = (64, 128, 256)  # split-KV decode/verify and tiled extend kernels
+MAX_HEAD_DIM = 512                 # other multiples of 16 up to this: the any-head-dim kernel
+HEAD_DIM_MULTIPLE = 16
+
+
+def head_dim_supported(head_dim: int) -> bool:
+    """Head dims the library serves: every multiple of 16 from 16 to 512 (64, 128 and 256 on
+    the tuned kernels, the rest on the any-head-dim kernel, which needs no workspace)."""
+    d = int(head_dim)
+    return HEAD_DIM_MULTIPLE <= d <= MAX_HEAD_DIM and d % HEAD_DIM_MULTIPLE == 0
 
 _WORKSPACES: dict = {}
 _DEVICE_WORKGROUPS: dict = {}
@@ -129,6 +138,13 @@ def workspace_buffer(device: torch.device, nbytes: int) -> torch.Tensor:
         buf = torch.zeros(cap, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = buf
     return buf
+
+
+def splitkv_workspace_bytes(device: torch.device, head_dim: int, num_workgroups: Optional[int] = None) -> int:
+    """Bytes of a split-KV workspace at this grid and head dim (0 for the head dims served
+    by the any-head-dim kernel)."""
+    nwg = int(num_workgroups) if num_workgroups else splitkv_workgroups(device)
+    return int(_lib.load().ma_splitkv_workspace_bytes(nwg, int(head_dim)))
 
 
 def splitkv_workspace(device: torch.device, num_workgroups: Optional[int] = None,

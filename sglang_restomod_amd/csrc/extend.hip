@@ -46,6 +46,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "paged_any.h"
 
 // MA_ASM_PIPELINE: the build verifies the generated code of this file for accesses to
 // registers whose inline-assembly loads are still in flight.
@@ -693,8 +694,9 @@ extern "C" int ma_paged_extend(
     int causal, int sliding_window, float softmax_scale, float k_scale, float v_scale,
     void* workspace, size_t workspace_bytes, void* out, int out_dtype, int64_t out_stride_tok,
     int64_t out_stride_head, void* stream) {
-  const int bm = extend_tile_rows(head_dim);
-  if (bm == 0) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (64, 128 or 256)", head_dim);
+  const bool generic = any_head_dim(head_dim);  // served by the any-head-dim kernel
+  const int bm = generic ? kAnyPlanRows : extend_tile_rows(head_dim);
+  if (bm == 0) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (multiples of 16 up to %d)", head_dim, kAnyMaxDim);
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
   if (kv_dtype < 0 || kv_dtype > DT_E5M2) return set_error(MA_EINVAL, "kv dtype %d unknown", kv_dtype);
   if ((kv_dtype == DT_F16 || kv_dtype == DT_BF16) && kv_dtype != q_dtype)
@@ -732,11 +734,27 @@ extern "C" int ma_paged_extend(
   p.num_tokens = (int)num_tokens;
   p.batch = batch; p.group = group; p.causal = causal ? 1 : 0; p.window = sliding_window < 0 ? -1 : sliding_window;
   p.tile_rows = bm;
-  p.tile_keys = head_dim == 256 ? XShape<256>::BN : XShape<128>::BN;
+  p.tile_keys = generic ? kAnyKeys : head_dim == 256 ? XShape<256>::BN : XShape<128>::BN;
   p.capacity = (int)items; p.items = reinterpret_cast<int64_t*>(workspace);
   hipLaunchKernelGGL(extend_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "extend plan launch failed: %s", hipGetErrorString(e));
+  if (generic) {
+    AnyArgs g{};
+    g.q = q; g.q_stride_tok = q_stride_tok; g.q_stride_head = q_stride_head;
+    g.k = k_cache; g.v = v_cache; g.kv_stride_row = kv_stride_row; g.kv_stride_head = kv_stride_head;
+    g.tt.table = table; g.tt.stride = table_stride; g.tt.page_shift = __builtin_ctz(page_size);
+    g.row_index = row_index; g.seq_lens = seq_lens; g.qsl = query_start_loc; g.prefix = prefix_lens;
+    g.num_tokens = (int)num_tokens; g.batch = batch; g.hq = num_q_heads; g.hkv = num_kv_heads; g.group = group;
+    g.head_dim = head_dim; g.items = p.items; g.row_blocks = 0;
+    g.causal = p.causal; g.window = p.window;
+    g.scale_log2 = softmax_scale * k_scale * kLog2e; g.v_scale = v_scale;
+    g.out = out; g.out_stride_tok = out_stride_tok; g.out_stride_head = out_stride_head;
+    g.out_f32 = out_dtype == DT_F32;
+    e = any_launch(g, q_dtype, kv_dtype, items * num_kv_heads, (hipStream_t)stream);
+    if (e != hipSuccess) return set_error(MA_ELAUNCH, "any-head-dim launch failed: %s", hipGetErrorString(e));
+    return MA_OK;
+  }
   ExtendArgs a{};
   a.q = q; a.q_stride_tok = q_stride_tok; a.q_stride_head = q_stride_head;
   a.k = k_cache; a.v = v_cache; a.kv_stride_row = kv_stride_row; a.kv_stride_head = kv_stride_head;

@@ -52,6 +52,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "paged_any.h"
 
 // MA_ASM_PIPELINE: the build verifies the generated code of this file for accesses to
 // registers whose inline-assembly loads are still in flight.
@@ -963,6 +964,7 @@ static constexpr size_t ws_bytes(int num_workgroups, int head_dim) {
 
 extern "C" size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim) {
   if (num_workgroups <= 0 || head_dim <= 0) return 0;
+  if (any_head_dim(head_dim)) return 0;  // the any-head-dim kernel keeps no partials
   return ws_bytes(num_workgroups, head_dim);
 }
 
@@ -1006,8 +1008,9 @@ extern "C" int ma_device_workgroups(void) { return device_workgroups(0); }
 
 static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, int max_q_per_seq,
                        int num_workgroups, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (64, 128 or 256)", head_dim);
+  const bool generic = any_head_dim(head_dim);  // served by the any-head-dim kernel
+  if (!generic && head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (multiples of 16 up to %d)", head_dim, kAnyMaxDim);
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
   if (kv_dtype < 0 || kv_dtype > DT_E5M2) return set_error(MA_EINVAL, "kv dtype %d unknown", kv_dtype);
   if ((kv_dtype == DT_F16 || kv_dtype == DT_BF16) && kv_dtype != q_dtype)
@@ -1034,6 +1037,24 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   a.group = a.hq / a.hkv;
   if ((int64_t)a.num_tokens * a.group > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens x GQA group exceeds 2^31");
+  if (generic) {
+    // no split over keys and no workspace: one wave per 16 rows (token, GQA head)
+    AnyArgs g{};
+    g.q = a.q; g.q_stride_tok = a.q_stride_tok; g.q_stride_head = a.q_stride_head;
+    g.k = a.k; g.v = a.v; g.kv_stride_row = a.kv_stride_row; g.kv_stride_head = a.kv_stride_head;
+    g.tt = a.tt; g.row_index = a.row_index; g.seq_lens = a.seq_lens; g.qsl = a.qsl; g.prefix = a.prefix;
+    g.num_tokens = a.num_tokens; g.batch = a.batch; g.hq = a.hq; g.hkv = a.hkv; g.group = a.group;
+    g.head_dim = head_dim; g.items = nullptr;
+    g.row_blocks = (int)(((int64_t)max_q_per_seq * a.group + kAnyRows - 1) / kAnyRows);
+    g.causal = a.causal; g.window = a.window; g.scale_log2 = a.scale_log2; g.v_scale = a.v_scale;
+    g.out = a.out; g.out_stride_tok = a.out_stride_tok; g.out_stride_head = a.out_stride_head; g.out_f32 = a.out_f32;
+    const int64_t wave_items = (int64_t)a.batch * a.hkv * g.row_blocks;
+    const int64_t grid = (wave_items + kAnyWaves - 1) / kAnyWaves;
+    if (grid > 0x7fffffff) return set_error(MA_EINVAL, "grid too large");
+    const hipError_t e = any_launch(g, q_dtype, kv_dtype, grid, stream);
+    if (e != hipSuccess) return set_error(MA_ELAUNCH, "any-head-dim launch failed: %s", hipGetErrorString(e));
+    return MA_OK;
+  }
   const int rows_total = max_q_per_seq * a.group;
   const int nb = (rows_total <= 16 || head_dim == 256) ? 1 : 2;
   a.rows = 16 * nb;
@@ -1127,7 +1148,7 @@ extern "C" int ma_grouped_decode_noalloc(
     void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
   if (num_workgroups <= 0 || num_workgroups > kScratchWorkgroups)
     return set_error(MA_EINVAL, "num_workgroups %d: the static scratch serves 1..%d", num_workgroups, kScratchWorkgroups);
-  if (head_dim > 256) return set_error(MA_EUNSUPPORTED, "head_dim %d exceeds the static scratch's 256", head_dim);
+  // head dims above 256 run on the any-head-dim kernel, which uses no scratch
   void* ws = nullptr;
   const int rc = scratch_of_current_device(&ws);
   if (rc != MA_OK) return rc;

@@ -32,13 +32,14 @@ def test_registry_factory_builds_the_backend():
     assert be.needs_cpu_seq_lens is False
 
 
-def test_unsupported_head_dim_is_refused_at_construction():
-    eng = _engine(head_dim=96)
+@pytest.mark.parametrize("head_dim", [100, 528])
+def test_unsupported_head_dim_is_refused_at_construction(head_dim):
+    eng = _engine(head_dim=head_dim)
     with pytest.raises(NotImplementedError, match="head_dim"):
         _backend(eng)
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("head_dim", [64, 128, 256, 16, 96, 192, 320, 512])
 def test_supported_head_dims_construct(head_dim):
     be = _backend(_engine(head_dim=head_dim))
     assert be.head_dim == head_dim

@@ -288,7 +288,8 @@ def test_supported_layer_has_no_reason():
 @pytest.mark.parametrize("kw,reason", [
     ({"tp_k_head_num": 7}, "gqa_ratio"),
     ({"v_head_dim": 64}, "qk_dim"),
-    ({"qk_head_dim": 96, "v_head_dim": 96}, "head_dim"),
+    ({"qk_head_dim": 250, "v_head_dim": 250}, "not_a_multiple"),
+    ({"qk_head_dim": 528, "v_head_dim": 528}, "head_dim"),
     ({"is_cross_attention": True}, "cross_attention"),
     ({"logit_cap": 30.0}, "logit_cap"),
     ({"xai_temperature_len": 8}, "xai_temperature"),

@@ -61,7 +61,8 @@ def _decode_args(**over):
 
 
 @pytest.mark.parametrize("over,msg", [
-    ({"dim": 96}, "head_dim"),
+    ({"dim": 100}, "head_dim"),
+    ({"dim": 528}, "head_dim"),
     ({"qdt": 2}, "q dtype"),
     ({"kvdt": 0}, "16-bit KV dtype must equal"),
     ({"hq": 12, "hkv": 8}, "head counts"),
@@ -86,6 +87,9 @@ def test_empty_batch_is_a_no_op(lib):
 
 def test_workspace_size_formula(lib):
     assert lib.ma_splitkv_workspace_bytes(0, 128) == 0
+    # the other head dims run on a kernel without a workspace
+    for d in (16, 96, 192, 320, 512):
+        assert lib.ma_splitkv_workspace_bytes(256, d) == 0
     n = lib.ma_splitkv_workspace_bytes(256, 128)
     # two partial pieces of up to 32 rows per wave, 4 waves per workgroup
     assert n >= 256 * 4 * 2 * 32 * 129 * 4 and n % 256 == 0
@@ -127,7 +131,8 @@ def _extend_args(**over):
 
 
 @pytest.mark.parametrize("over,msg", [
-    ({"dim": 96}, "head_dim"),
+    ({"dim": 100}, "head_dim"),
+    ({"dim": 528}, "head_dim"),
     ({"qdt": 3}, "q dtype"),
     ({"kvdt": 0}, "16-bit KV dtype must equal"),
     ({"hq": 12, "hkv": 8}, "head counts"),

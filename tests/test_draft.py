@@ -122,7 +122,8 @@ LAYERS = [fakes.Layer(8, 2)]
     ({}, 1, (128, 0), LAYERS, "draft-decode window"),
     ({}, 1, (0, 4), LAYERS, "sink=4"),
     ({"kv_index_translator": SimpleNamespace(is_translating=True)}, 1, (0, 0), LAYERS, "KV index translation"),
-    ({}, 1, (0, 0), [fakes.Layer(8, 2, head_dim=96)], "head_dim(96)"),
+    ({}, 1, (0, 0), [fakes.Layer(8, 2, head_dim=100)], "dim(100)_not_a_multiple_of_16"),
+    ({}, 1, (0, 0), [fakes.Layer(8, 2, head_dim=528)], "head_dim(528)"),
     ({}, 1, (0, 0), [fakes.Layer(8, 3)], "gqa_ratio"),
 ])
 def test_support_gaps(over, topk, window, layers, gap):
@@ -212,5 +213,5 @@ def test_container_sizes_its_workspace_for_the_model_head_dim():
     cont = draft_decode.MI355XMultiStepDraftBackend(eng.runner, 1, 3, layers=[fakes.Layer(8, 2, head_dim=256)])
     assert cont.head_dim == 256
     bare = SimpleNamespace(**{k: v for k, v in vars(_runner()).items() if k != "model_config"})
-    assert draft_decode.MI355XMultiStepDraftBackend(bare, 1, 3, layers=LAYERS).head_dim == \
-        max(draft_decode_plan.SUPPORTED_HEAD_DIMS)
+    # without a model head dim: the one with the largest split-KV workspace
+    assert draft_decode.MI355XMultiStepDraftBackend(bare, 1, 3, layers=LAYERS).head_dim == 256

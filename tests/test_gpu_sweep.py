@@ -6,7 +6,8 @@ none. Slots are a random permutation of a shared pool, and the table rows are
 permuted inside a larger ``req_to_token``. The same case runs through the split-KV
 decode (the last token of each sequence), the split-KV verify (up to 16 rows per
 sequence) and the MFMA extend (any number of rows). The sizes keep the oracle fast.
-The head dim is 128 except in the ``headdim`` cases, which run 64 and 256.
+The head dim is 128 except in the ``headdim`` cases, which run 64 and 256, and the
+``anydim`` cases, which run other multiples of 16 up to 512.
 """
 
 from __future__ import annotations
@@ -174,4 +175,30 @@ def test_sweep_headdim_verify(dim, seed):
 @pytest.mark.parametrize("seed", range(6))
 def test_sweep_headdim_decode(dim, seed):
     c = _decode_case(6000 + seed, dim=dim)
+    assert_attn_close(_run_decode(c), _reference(c), what=f"decode D={dim} seed {seed}")
+
+
+# Head dims outside 64/128/256 run on the any-head-dim kernel (one wave per 16 rows, the
+# kernel padded to the next of 64/128/256/512): multiples of 16 across that range.
+ANY_DIMS = [16, 48, 80, 96, 160, 192, 320, 448, 512]
+
+
+@pytest.mark.parametrize("dim", ANY_DIMS)
+@pytest.mark.parametrize("seed", range(2))
+def test_sweep_anydim_extend(dim, seed):
+    c = _build(7000 + 10 * ANY_DIMS.index(dim) + seed, max_q=200, dim=dim)
+    assert_attn_close(_run_extend(c), _reference(c), what=f"extend D={dim} seed {seed}")
+
+
+@pytest.mark.parametrize("dim", ANY_DIMS)
+@pytest.mark.parametrize("seed", range(2))
+def test_sweep_anydim_verify(dim, seed):
+    c = _build(8000 + 10 * ANY_DIMS.index(dim) + seed, max_q=16, dim=dim)
+    assert_attn_close(_run_verify(c), _reference(c), what=f"verify D={dim} seed {seed}")
+
+
+@pytest.mark.parametrize("dim", ANY_DIMS)
+@pytest.mark.parametrize("seed", range(2))
+def test_sweep_anydim_decode(dim, seed):
+    c = _decode_case(9000 + 10 * ANY_DIMS.index(dim) + seed, dim=dim)
     assert_attn_close(_run_decode(c), _reference(c), what=f"decode D={dim} seed {seed}")
