@@ -16,7 +16,9 @@ extend TFLOP/s against the bf16 MFMA roofline), so one JSON line carries:
 * ``fp8_decode``: workload 3 (B=128, ctx U[4096, 32768], 32 / 8 heads) over e4m3 and
   e5m2 pools; ``verify``: workload 4 (B=32, 4 draft tokens, P U[2048, 16384], 64 / 8
   heads); ``decode_b1``: workload 0's latency; ``kv_write``: the pool write of the
-  extend batch into an e4m3 pool. ``--headline-only`` skips all of these.
+  extend batch into an e4m3 pool; ``head_dim_256`` and ``head_dim_512``: decode and
+  extend at head dims 256 (workloads 5, 6) and 512 (7, 8). ``--headline-only`` skips all
+  of these.
 
 ``value`` is whole-job throughput: algorithmic bytes of the K timed steps over
 the wall time between the two synchronisations. Warm-up is W untimed steps and
@@ -350,8 +352,9 @@ def _roofline(r, kernel, bound_hbm):
         "frac": round(achieved / peak, 4),
         "traffic": _traffic(kernel, r["profile_name"]),
         "kernel_ms": round(r["event_ms_mean"], 5),
-        "timing": ("HIP events on the launch stream around each call (split-KV partial + merge)" if bound_hbm
-                   else "HIP events on the launch stream around each call (plan + extend kernel)"),
+        "timing": "HIP events on the launch stream around each call ("
+                  + ("any-head-dim kernel" + ("" if bound_hbm else ", after the work-list plan") if kernel == "any_kernel"
+                     else "split-KV partial + merge" if bound_hbm else "plan + extend kernel") + ")",
     }
     if bound_hbm:
         ceil = r["gather_ceiling_GBps"]
@@ -437,6 +440,12 @@ def main():
             line["decode_b1"] = {"workload": r["workload"], "us_per_call": round(r["event_ms_mean"] * 1e3, 2),
                                  "wall_us_per_call": round(r["ms_per_step"] * 1e3, 2)}
         line["kv_write"] = _measure_kv_write(steps, args.warmup)
+        # the other head dims of the reference's tuned configurations: 256 on the split-KV and
+        # tiled extend kernels, 512 on the any-head-dim kernel
+        line["head_dim_256"] = {"decode": _family(_measure(5, steps, args.warmup, 0), "splitkv_partial", True),
+                                "extend": _family(_measure(6, steps, args.warmup, 0), "extend_kernel", False)}
+        line["head_dim_512"] = {"decode": _family(_measure(7, steps, args.warmup, 0), "any_kernel", True),
+                                "extend": _family(_measure(8, steps, args.warmup, 0), "any_kernel", False)}
     print(json.dumps(line))
 
 

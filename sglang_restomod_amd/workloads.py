@@ -1,5 +1,5 @@
-"""Seeded generators for the benchmark workloads: five at head dim 128 (0-4) and two
-at head dim 256 (5, 6).
+"""Seeded generators for the benchmark workloads: five at head dim 128 (0-4), two at
+head dim 256 (5, 6) and two at head dim 512 (7, 8).
 
 Seeding scheme: one CPU ``torch.Generator`` per workload with seed = workload
 index. Draw order: lengths, slot permutation, then (on the target device,
@@ -37,6 +37,11 @@ WORKLOADS = {
             heads=12, heads_kv=2, dim=256, dtype="bf16", kv="bf16"),
     6: dict(name="extend_b8_p0-4k_e256-2k_h12kv2_d256_bf16", mode="extend", batch=8,
             prefix=(0, 4096), extend=(256, 2048), heads=12, heads_kv=2, dim=256, dtype="bf16", kv="bf16"),
+    # head dim 512 (the reference's widest tuned configuration), on the any-head-dim kernel
+    7: dict(name="decode_b64_ctx1k-8k_h16kv4_d512_bf16", mode="decode", batch=64, ctx=(1024, 8192),
+            heads=16, heads_kv=4, dim=512, dtype="bf16", kv="bf16"),
+    8: dict(name="extend_b8_p0-4k_e256-2k_h16kv4_d512_bf16", mode="extend", batch=8,
+            prefix=(0, 4096), extend=(256, 2048), heads=16, heads_kv=4, dim=512, dtype="bf16", kv="bf16"),
 }
 
 _DT = {"fp16": torch.float16, "bf16": torch.bfloat16}

@@ -7,7 +7,8 @@
   (an exact result rounded to bf16 is already up to half an ulp away).
 
 Workloads: decode B=1 (fp16), decode B=64 (bf16), fp8 decode B=128 in e4m3 and e5m2,
-verify B=32 x 4, extend B=8 (every row), and the head-dim-256 decode and extend.
+verify B=32 x 4, extend B=8 (every row), and the head-dim-256 and head-dim-512 decode
+and extend.
 """
 
 from __future__ import annotations
@@ -53,7 +54,8 @@ def _half_ulp(ref: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return 0.5 * torch.exp2(torch.floor(torch.log2(mag)) - mant)
 
 
-CASES = [(0, "e4m3"), (1, "e4m3"), (3, "e4m3"), (3, "e5m2"), (4, "e4m3"), (2, "e4m3"), (5, "e4m3"), (6, "e4m3")]
+CASES = [(0, "e4m3"), (1, "e4m3"), (3, "e4m3"), (3, "e5m2"), (4, "e4m3"), (2, "e4m3"), (5, "e4m3"), (6, "e4m3"),
+         (7, "e4m3"), (8, "e4m3")]
 
 
 @pytest.mark.parametrize("index,fmt", CASES)
