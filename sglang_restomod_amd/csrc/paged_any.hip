@@ -50,13 +50,31 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
   static_assert(!kFp8 || KK % 2 == 0, "fp8 K loads cover two QK steps");
   typedef typename AnyVRaw<kFp8>::type VRaw;
 
-  __shared__ __attribute__((aligned(256))) unsigned char vlds[kAnyWaves][kAnyKeys * kRowL];
   // At the widest head dim with 16-bit KV, Q lives in LDS (rows padded by 16 bytes so the
   // 16 rows of an operand read fall in different banks): its 64 registers are what the
   // prefetched K and V need.
   constexpr bool kQLds = DP >= 512 && !kFp8;
   constexpr int kQRow = DP * 2 + 16;
-  __shared__ __attribute__((aligned(256))) unsigned char qlds[kQLds ? kAnyWaves : 1][kQLds ? kAnyRows * kQRow : 16];
+  constexpr int kVBlock = kAnyKeys * kRowL;            // one wave's V rows
+  constexpr int kQBlock = kQLds ? kAnyRows * kQRow : 0;  // one wave's Q rows
+  constexpr int kSmem = kAnyWaves * (kVBlock + kQBlock);
+  // When the four waves split one row block's keys, their partial O meet in the same
+  // memory after the loop, kBPR 16-column blocks (1 KiB per wave each) at a time.
+  constexpr int kBPR = (DB * kAnyWaves * 1024 <= kSmem) ? DB
+                       : (DB / 2 * kAnyWaves * 1024 <= kSmem) ? DB / 2
+                       : (DB / 4 * kAnyWaves * 1024 <= kSmem) ? DB / 4 : DB / 8;
+  static_assert(kBPR >= 1 && kBPR * kAnyWaves * 1024 <= kSmem, "merge rounds fit the V/Q memory");
+  // Extend rows: the four waves own 64 consecutive rows of one sequence and kv head and
+  // share every K/V tile through a two-stage LDS ring (16-bit K rows padded by 16 bytes,
+  // fp16 V rows as above), loaded once per workgroup; kUW 16-byte units per thread.
+  constexpr int kRowK = DP * 2 + 16;
+  constexpr int kKTile = kAnyKeys * kRowK;
+  constexpr int kStageB = kKTile + kVBlock;
+  constexpr int kTileUnits = kAnyKeys * kUnits;  // 16-byte units of one K (or V) tile
+  constexpr int kUW = kTileUnits >= kAnyWaves * 64 ? kTileUnits / (kAnyWaves * 64) : 1;
+  static_assert(2 * kStageB <= kAnyWaves * kVBlock, "the ring fits the per-wave V memory it replaces");
+  __shared__ __attribute__((aligned(256))) unsigned char smem[kSmem];
+  __shared__ float mrow[kAnyWaves][2][kAnyRows];  // each wave's row max and row sum of p
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -64,8 +82,9 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
   const int j = lane >> 4;
   const int D = a.head_dim;
   const int G = a.group;
-  unsigned char* my_lds = vlds[wave];
-  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)my_lds;
+  const uint32_t smem_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
+  const uint32_t lds_base = smem_base + wave * kVBlock;                          // this wave's V rows
+  const uint32_t q_base = smem_base + kAnyWaves * kVBlock + wave * kQBlock;      // and Q rows
 
   // first dim of QK step kk for lane group j (fp8: one 16-byte load covers two steps)
   auto qdim = [&](int kk) -> int {
@@ -77,8 +96,14 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
   const int64_t row_bytes = a.kv_stride_row * kElt;
   const int page_mask = (1 << a.tt.page_shift) - 1;
 
-  // One wave's 16 rows r0 .. r0 + 15 of sequence b, kv head h.
-  auto rows = [&](int b, int h, int r0) __attribute__((always_inline)) {
+  // One wave's 16 rows r0 .. r0 + 15 of sequence b, kv head h. split < 0: the workgroup's
+  // four waves own consecutive row blocks (rows r0 - 16 * wave ..) and walk the keys any
+  // of them sees together, sharing each K/V tile. split >= 0: the four waves own the same
+  // row block and take quarter `split` of its key tiles each, merging at the end.
+  auto rows = [&](int b, int h, int r0, int split) __attribute__((always_inline)) {
+    const bool shared = split < 0;
+    const int rg0 = shared ? r0 - wave * kAnyRows : r0;  // first row of the workgroup's rows
+    const int rgn = shared ? kAnyWaves * kAnyRows : kAnyRows;
     int tok0, ntok;
     if (a.qsl) {
       const QueryRows qr = clamp_query_rows(cptr(a.qsl)[b], cptr(a.qsl)[b + 1], a.num_tokens);
@@ -88,7 +113,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       tok0 = b;
       ntok = b < a.num_tokens ? 1 : 0;
     }
-    if (r0 >= ntok * G) return;
+    if (rg0 >= ntok * G) return;  // the same for every wave of the workgroup
     const int seq = max(cptr(a.seq_lens)[b], 0);
     const int prefix = a.prefix ? cptr(a.prefix)[b] : seq - ntok;
     const int64_t seq_row = a.row_index ? cptr(a.row_index)[b] : (int64_t)b;
@@ -103,26 +128,27 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
     const int lo_r = (real && a.window >= 0) ? max(0, qpos - a.window) : 0;
     const int hi_r = real ? (a.causal ? min(seq, qpos + 1) : seq) : 0;
     u32x4 qv[kQLds ? 1 : KK];
-    const uint32_t qa = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)qlds[kQLds ? wave : 0] +
-                        c * kQRow + j * 16;
+    const uint32_t qa = q_base + c * kQRow + j * 16;
     {
       const uint16_t MA_GLOBAL* qp = gptr(reinterpret_cast<const uint16_t*>(a.q)) +
                                      (int64_t)(tok0 + (real ? t : 0)) * a.q_stride_tok +
                                      (int64_t)(h * G + g) * a.q_stride_head;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        const int d0 = qdim(kk);
+        const int d0 = shared ? kk * 32 + j * 8 : qdim(kk);
         const u32x4 qf = (real && d0 < D) ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + d0) : u32x4{0, 0, 0, 0};
         if constexpr (kQLds) *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(qa + kk * 64)) = qf;
         else qv[kk] = qf;
       }
     }
-    // keys any of the 16 rows may see
-    const int t_first = r0 / G;
-    const int t_last = min(ntok - 1, (r0 + kAnyRows - 1) / G);
+    // keys any of the rows (the wave's, or the workgroup's in shared mode) may see
+    const int t_first = rg0 / G;
+    const int t_last = min(ntok - 1, (rg0 + rgn - 1) / G);
     const int key_lo = a.window >= 0 ? max(0, prefix + t_first - a.window) : 0;
     const int key_hi = a.causal ? min(seq, prefix + t_last + 1) : seq;
     const int nt = key_hi > key_lo ? (key_hi - key_lo + kAnyKeys - 1) / kAnyKeys : 0;
+    const int i_lo = shared ? 0 : split * nt / kAnyWaves;
+    const int i_hi = shared ? nt : (split + 1) * nt / kAnyWaves;
 
     float m_run = -INFINITY;
     float lsum = 0.f;  // this lane's share of its row's sum of p (keys 4j .. 4j + 3 of each tile)
@@ -206,8 +232,24 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       }
       return s;
     };
-    // softmax and PV of tile i (its V already in LDS)
-    auto finish = [&](int i, f32x4 s) __attribute__((always_inline)) {
+    // scores of tile i from a K tile in LDS (shared mode)
+    auto scores_lds = [&](uint32_t kt) __attribute__((always_inline)) -> f32x4 {
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint32_t ka0 = kt + c * kRowK + j * 16;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const u32x4 kf = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(ka0 + kk * 64));
+        if constexpr (kQLds) {
+          const u32x4 qf = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(qa + kk * 64));
+          s = mfma16t<QBF16>(kf, qf, s);
+        } else {
+          s = mfma16t<QBF16>(kf, qv[kk], s);
+        }
+      }
+      return s;
+    };
+    // softmax and PV of tile i (its V in LDS at vt)
+    auto finish = [&](int i, f32x4 s, uint32_t vt) __attribute__((always_inline)) {
       const int kb0 = key_lo + i * kAnyKeys + 4 * j;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -232,7 +274,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       lsum += (p[0] + p[1]) + (p[2] + p[3]);
       const u32x2 pk = u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
       // O^T[d][row] += V^T[d][key] P^T[key][row], 16 dims per step
-      const uint32_t vb = lds_base + (4 * j + (c >> 2)) * kRowL + (c & 3) * 8;
+      const uint32_t vb = vt + (4 * j + (c >> 2)) * kRowL + (c & 3) * 8;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const uint32_t addr = vb + db * 32;
@@ -243,7 +285,82 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       }
     };
 
-    if (nt > 0) {
+    if (shared && nt > 0) {
+      // The workgroup's tile ring. Step i writes tile i+1 (loaded during step i-1) to stage
+      // (i+1) % 2, loads tile i+2, computes tile i from stage i % 2, then meets the other
+      // waves: the barrier publishes stage (i+1) % 2 and retires stage i % 2. Tiles past
+      // the last are the last again (key positions clamp), every load is unconditional.
+      u32x4 kraw0[kUW], kraw1[kUW];
+      VRaw vraw0[kUW], vraw1[kUW];
+      auto load_units = [&](int myslot, u32x4 (&kraw)[kUW], VRaw (&vraw)[kUW]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int x = 0; x < kUW; ++x) {
+          const int u = min((int)threadIdx.x + kAnyWaves * 64 * x, kTileUnits - 1);
+          const int key = u / kUnits;
+          const int q = min(u - key * kUnits, D / 8 - 1);
+          const int64_t off = (int64_t)shfl_i(myslot, key) * row_bytes + head_off + q * 8 * kElt;
+          if constexpr (kFp8) {
+            const u32x2 w = *reinterpret_cast<const u32x2 MA_GLOBAL*>(kbase + off);
+            kraw[x] = u32x4{w[0], w[1], 0u, 0u};
+          } else {
+            kraw[x] = *reinterpret_cast<const u32x4 MA_GLOBAL*>(kbase + off);
+          }
+          vraw[x] = *reinterpret_cast<const VRaw MA_GLOBAL*>(vbase + off);
+        }
+      };
+      auto write_units = [&](uint32_t st, const u32x4 (&kraw)[kUW], const VRaw (&vraw)[kUW]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int x = 0; x < kUW; ++x) {
+          const int u = (int)threadIdx.x + kAnyWaves * 64 * x;
+          if (u < kTileUnits) {
+            const int key = u / kUnits;
+            const int q = u - key * kUnits;
+            u32x4 kh, vh;
+            if constexpr (kFp8) {
+              kh = cvt8_fp8<KV, QBF16>(kraw[x][0], kraw[x][1]);
+              vh = cvt8_fp8<KV, false>(vraw[x][0], vraw[x][1]);
+            } else {
+              kh = kraw[x];
+              if constexpr (QBF16) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                  vh[w] = pack_f16(__builtin_bit_cast(float, vraw[x][w] << 16),
+                                   __builtin_bit_cast(float, vraw[x][w] & 0xffff0000u));
+              } else {
+                vh = vraw[x];
+              }
+            }
+            *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(st + key * kRowK + q * 16)) = kh;
+            *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(st + kKTile + key * kRowL + q * 16)) = vh;
+          }
+        }
+      };
+      auto stage = [&](int i) -> uint32_t { return smem_base + (i & 1) * kStageB; };
+      // tile t's raw units live in buffer t % 2 from the step that loads them (t - 3) to
+      // the step that writes them to LDS (t - 1): two tiles' compute to land in
+      int pg = page_load(0);
+      load_units(slot_of(0, pg), kraw0, vraw0);
+      pg = page_load(1);
+      load_units(slot_of(1, pg), kraw1, vraw1);
+      pg = page_load(2);
+      write_units(stage(0), kraw0, vraw0);
+      load_units(slot_of(2, pg), kraw0, vraw0);
+      pg = page_load(3);
+      __syncthreads();
+      auto tile_step = [&](int i, u32x4 (&kn)[kUW], VRaw (&vn)[kUW]) __attribute__((always_inline)) {
+        write_units(stage(i + 1), kn, vn);       // tile i+1, buffer (i+1) % 2
+        load_units(slot_of(i + 3, pg), kn, vn);  // tile i+3 into the buffer just written
+        pg = page_load(i + 4);
+        finish(i, scores_lds(stage(i)), stage(i) + kKTile);
+        __syncthreads();
+      };
+#pragma unroll 1
+      for (int i = 0; i < nt; i += 2) {
+        tile_step(i, kraw1, vraw1);
+        if (i + 1 < nt) tile_step(i + 1, kraw0, vraw0);
+      }
+    }
+    if (!shared && i_hi > i_lo) {
       // Step i issues the slot lookup of tile i+2, writes tile i's V to LDS and refills the
       // V registers with tile i+1, and loads tile i+1's K (into the other K buffer, or at
       // the widest head dims into the same one once tile i's scores have used it), so every
@@ -252,10 +369,10 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       constexpr bool kTwoK = DP <= 256;
       u32x4 ka[kKL], kb[kKL];
       VRaw vr[kUL];
-      int page1 = page_load(0);
-      load_v(slot_of(0, page1), vr);
-      load_k(slot_of(0, page1), ka);
-      page1 = page_load(1);
+      int page1 = page_load(i_lo);
+      load_v(slot_of(i_lo, page1), vr);
+      load_k(slot_of(i_lo, page1), ka);
+      page1 = page_load(i_lo + 1);
       int page2;
       auto step = [&](int i, u32x4 (&kc)[kKL], u32x4 (&kn)[kKL]) __attribute__((always_inline)) {
         page2 = page_load(i + 2);
@@ -270,17 +387,17 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
           s = scores(kc);
           load_k(sn, kc);
         }
-        finish(i, s);
+        finish(i, s, lds_base);
         page1 = page2;
       };
 #pragma unroll 1
-      for (int i = 0; i < nt; i += 2) {
+      for (int i = i_lo; i < i_hi; i += 2) {
         if constexpr (kTwoK) {
           step(i, ka, kb);
-          if (i + 1 < nt) step(i + 1, kb, ka);
+          if (i + 1 < i_hi) step(i + 1, kb, ka);
         } else {
           step(i, ka, ka);
-          if (i + 1 < nt) step(i + 1, ka, ka);
+          if (i + 1 < i_hi) step(i + 1, ka, ka);
         }
       }
     }
@@ -288,14 +405,54 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
     // normalise and store this lane's row: dims db * 16 + 4j .. + 3
     float lt = lsum + shfl_xor_f(lsum, 16);
     lt += shfl_xor_f(lt, 32);
-    if (real) {
-      const float inv = (lt > 0.f) ? a.v_scale / lt : 0.f;
-      const int64_t off = (int64_t)(tok0 + t) * a.out_stride_tok + (int64_t)(h * G + g) * a.out_stride_head;
+    const int64_t off = (int64_t)(tok0 + t) * a.out_stride_tok + (int64_t)(h * G + g) * a.out_stride_head;
+    if (shared) {
+      if (real) {
+        const float inv = (lt > 0.f) ? a.v_scale / lt : 0.f;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        if (db * 16 >= D) break;
-        store_out4<QBF16>(a.out, off + db * 16 + 4 * j, o[db], inv, a.out_f32);
+        for (int db = 0; db < DB; ++db) {
+          if (db * 16 >= D) break;
+          store_out4<QBF16>(a.out, off + db * 16 + 4 * j, o[db], inv, a.out_f32);
+        }
       }
+      return;
+    }
+    // merge of the four quarters: each O and row sum is relative to its wave's exponent
+    // base (its row max, 0 when it saw no key), rescaled to the largest
+    if (j == 0) {
+      mrow[wave][0][c] = m_run;
+      mrow[wave][1][c] = lt;
+    }
+    __syncthreads();  // every wave is done with its V/Q memory, which the merge reuses
+    float mmax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kAnyWaves; ++u) mmax = fmaxf(mmax, mrow[u][0][c]);
+    float sc[kAnyWaves];
+    float ltot = 0.f;
+#pragma unroll
+    for (int u = 0; u < kAnyWaves; ++u) {
+      const float mu = mrow[u][0][c];
+      sc[u] = (mu == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((mu - mmax) * a.scale_log2);
+      ltot += mrow[u][1][c] * sc[u];
+    }
+    const float inv = (ltot > 0.f) ? a.v_scale / ltot : 0.f;
+#pragma unroll
+    for (int r = 0; r < DB; r += kBPR) {
+#pragma unroll
+      for (int blk = 0; blk < kBPR; ++blk)
+        *reinterpret_cast<__attribute__((address_space(3))) f32x4*>(
+            (uintptr_t)(smem_base + ((wave * kBPR + blk) * 64 + lane) * 16)) = o[r + blk];
+      __syncthreads();
+      // this wave finishes the round's blocks wave, wave + 4, ...
+      for (int blk = wave; blk < kBPR; blk += kAnyWaves) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < kAnyWaves; ++u)
+          acc += *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(
+                     (uintptr_t)(smem_base + ((u * kBPR + blk) * 64 + lane) * 16)) * sc[u];
+        if (real && (r + blk) * 16 < D) store_out4<QBF16>(a.out, off + (r + blk) * 16 + 4 * j, acc, inv, a.out_f32);
+      }
+      __syncthreads();  // before the next round (or the next row block) reuses the memory
     }
   };
 
@@ -309,13 +466,14 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
     const int rt = (int)(work >> 32);
 #pragma unroll 1
     for (int pass = 0; pass < kAnyPlanRows / (kAnyWaves * kAnyRows); ++pass)
-      rows(b, h, rt * kAnyPlanRows + pass * (kAnyWaves * kAnyRows) + wave * kAnyRows);
+      rows(b, h, rt * kAnyPlanRows + pass * (kAnyWaves * kAnyRows) + wave * kAnyRows, -1);
   } else {
-    // wave item w: kv head w % hkv, then 16-row block, then sequence; a sequence with more
-    // rows than row_blocks blocks has its later blocks taken by the same wave in turn
-    const int64_t w = (int64_t)blockIdx.x * kAnyWaves + wave;
-    const int h = (int)(w % a.hkv);
-    const int64_t rest = w / a.hkv;
+    // decode and verify: workgroup item = (kv head, 16-row block, sequence), kv head
+    // fastest; its four waves take the four quarters of the rows' key tiles. A sequence
+    // with more rows than row_blocks blocks has its later blocks taken in turn.
+    const int64_t item = blockIdx.x;
+    const int h = (int)(item % a.hkv);
+    const int64_t rest = item / a.hkv;
     const int b = (int)(rest / a.row_blocks);
     const int rb = (int)(rest - (int64_t)b * a.row_blocks);
     if (b >= a.batch) return;
@@ -323,7 +481,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
     if (a.qsl) rows_b = clamp_query_rows(cptr(a.qsl)[b], cptr(a.qsl)[b + 1], a.num_tokens).ntok * a.group;
     else rows_b = (b < a.num_tokens ? 1 : 0) * a.group;
 #pragma unroll 1
-    for (int r0 = rb * kAnyRows; r0 < rows_b; r0 += a.row_blocks * kAnyRows) rows(b, h, r0);
+    for (int r0 = rb * kAnyRows; r0 < rows_b; r0 += a.row_blocks * kAnyRows) rows(b, h, r0, wave);
   }
 }
 

@@ -1038,7 +1038,8 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
   a.group = a.hq / a.hkv;
   if ((int64_t)a.num_tokens * a.group > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens x GQA group exceeds 2^31");
   if (generic) {
-    // no split over keys and no workspace: one wave per 16 rows (token, GQA head)
+    // no workspace: one workgroup per 16 rows (token, GQA head), its four waves splitting
+    // the keys and merging through LDS
     AnyArgs g{};
     g.q = a.q; g.q_stride_tok = a.q_stride_tok; g.q_stride_head = a.q_stride_head;
     g.k = a.k; g.v = a.v; g.kv_stride_row = a.kv_stride_row; g.kv_stride_head = a.kv_stride_head;
@@ -1048,8 +1049,7 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
     g.row_blocks = (int)(((int64_t)max_q_per_seq * a.group + kAnyRows - 1) / kAnyRows);
     g.causal = a.causal; g.window = a.window; g.scale_log2 = a.scale_log2; g.v_scale = a.v_scale;
     g.out = a.out; g.out_stride_tok = a.out_stride_tok; g.out_stride_head = a.out_stride_head; g.out_f32 = a.out_f32;
-    const int64_t wave_items = (int64_t)a.batch * a.hkv * g.row_blocks;
-    const int64_t grid = (wave_items + kAnyWaves - 1) / kAnyWaves;
+    const int64_t grid = (int64_t)a.batch * a.hkv * g.row_blocks;  // one workgroup per row block
     if (grid > 0x7fffffff) return set_error(MA_EINVAL, "grid too large");
     const hipError_t e = any_launch(g, q_dtype, kv_dtype, grid, stream);
     if (e != hipSuccess) return set_error(MA_ELAUNCH, "any-head-dim launch failed: %s", hipGetErrorString(e));
