@@ -1,7 +1,7 @@
 // Measurement kernel (not part of the attention library): the HBM read bandwidth of
 // gathering rows of a token pool [num_tokens, heads, row_bytes] from random slots, with
 // no arithmetic. It gives an attainable rate for the KV access pattern of paged decode
-// with page size 1: rows of one kv head (64 to 512 B: D=128 in 16 bits is 256 B) at
+// with page size 1: rows of one kv head (64 to 1024 B: D=128 in 16 bits is 256 B) at
 // random pool slots, each row read once per kv head, in the decode's head-major order.
 //
 // Workgroup (x, h): 4 waves; a wave reads the rows of head h for chunks_per_wave chunks of
@@ -75,7 +75,10 @@ extern "C" int ma_gather_ceiling(const void* pool, const int32_t* perm, int64_t 
   const dim3 grid((unsigned)bx, (unsigned)heads);
   const unsigned char* p = reinterpret_cast<const unsigned char*>(pool);
   hipStream_t st = (hipStream_t)stream;
-  if (row_bytes == 512)
+  if (row_bytes == 1024)
+    hipLaunchKernelGGL(gather_ceiling_kernel<1024>, grid, dim3(kThreads), 0, st, p, perm, num_tokens, heads,
+                       chunks_per_wave, sink);
+  else if (row_bytes == 512)
     hipLaunchKernelGGL(gather_ceiling_kernel<512>, grid, dim3(kThreads), 0, st, p, perm, num_tokens, heads,
                        chunks_per_wave, sink);
   else if (row_bytes == 256)
