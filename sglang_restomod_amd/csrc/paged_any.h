@@ -10,7 +10,7 @@
 
 namespace ma {
 
-constexpr int kAnyWaves = 4;        // waves per workgroup, each on its own rows
+constexpr int kAnyWaves = 4;        // waves per workgroup
 constexpr int kAnyRows = 16;        // query rows per wave
 constexpr int kAnyKeys = 16;        // keys per tile
 constexpr int kAnyPlanRows = 128;   // rows of one work-list entry (the extend plan's smallest tile)
@@ -30,8 +30,8 @@ struct AnyArgs {
   int num_tokens;            // rows of q and out: query rows are clamped into [0, num_tokens)
   int batch, hq, hkv, group;
   int head_dim;              // D: the kernel's width is the next of 64, 128, 256, 512
-  const int64_t* items;      // work list of 128-row tiles (extend), or null:
-  int row_blocks;            //   wave item w -> kv head w % hkv, 16-row block, sequence
+  const int64_t* items;      // work list of 128-row tiles (extend), or null: workgroup
+  int row_blocks;            //   item -> (kv head, 16-row block of row_blocks, sequence)
   int causal, window;
   float scale_log2;          // softmax_scale * k_scale * log2(e)
   float v_scale;

@@ -4,18 +4,21 @@
 // sglang_restomod/attention/v100/tilelang/_kernels_paged.py:397-418; above 256 its linear
 // verify also runs on the ordinary paged kernel, _paged_adapter.py:612-616).
 //
-// One kernel serves decode, linear verify and extend rows. Each wave owns 16 query rows
-// (token, GQA head) of one sequence and kv head and walks the keys those rows may see in
-// 16-key tiles, independently of the other waves of its workgroup:
-//   - K rows go from HBM straight into MFMA operand registers (16x16x32, the query's
-//     16-bit type; fp8 rows converted in registers),
-//   - V rows go to registers, are converted to fp16 and written to the wave's own LDS
-//     block, and are read back transposed (ds_read_b64_tr_b16) as the A operand of a
-//     16x16x16 fp16 MFMA whose B operand is the lane's own four probabilities,
-//   - the online softmax keeps the tuned kernels' lazy rescale (kLazyRescale).
-// The kernel is as wide as the next of 64, 128, 256 and 512: dims past the head dim load
-// as zero and are never stored. The slots of tile i+2 and the K/V of tile i+1 are loaded
-// before tile i is computed, so a tile's HBM round trip overlaps the previous tile.
+// One kernel serves decode, linear verify and extend rows. A wave computes 16 query rows
+// (token, GQA head) of one sequence and kv head over 16-key tiles:
+//   - scores S^T = K Q^T on 16x16x32 MFMAs (the query's 16-bit type; fp8 K converted),
+//     so each lane holds four keys of one row: the B operand of the 16x16x16 fp16 MFMA
+//     of O^T += V^T P^T, whose A operand is read transposed (ds_read_b64_tr_b16) from
+//     fp16 V rows in LDS,
+//   - an online softmax with the tuned kernels' lazy rescale (kLazyRescale).
+// Decode and verify (no work list): the four waves of a workgroup hold the same 16 rows
+// and take a quarter of their key tiles each, K straight into operand registers and V
+// through the wave's own LDS rows, then merge through LDS. Extend (the work list): the
+// four waves hold 64 consecutive rows and share each K/V tile through a two-stage LDS
+// ring, one barrier per tile.
+// The kernel is as wide as the next of 64, 128, 256 and 512: lanes past the head dim
+// read the row's last dims again (every load is unconditional), which meet Q's zeros in
+// the scores and fill output dims that are never stored.
 #include "capi_internal.h"
 #include "paged_any.h"
 
