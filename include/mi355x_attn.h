@@ -204,7 +204,7 @@ int ma_paged_extend(const void* q, int64_t q_stride_tok, int64_t q_stride_head, 
  * flash_attn_v100_backend.py:1174-1182 and 1038-1046, draft_decode.py:132-139) with
  * SGLang's token-pool semantics: row t of k and v ([num_tokens, num_kv_heads, head_dim],
  * src_dtype MA_DT_F16 / MA_DT_BF16, any token/head stride, head_dim contiguous and a
- * power of two in 8..2048) is stored at pool slot loc[t] of k_cache / v_cache.
+ * multiple of 8 in 8..2048) is stored at pool slot loc[t] of k_cache / v_cache.
  *   cache_dtype = src_dtype: a copy (scales ignored).
  *   otherwise: if apply_scale, x / scale in fp32 rounded to src_dtype, then cast to the
  *     cache dtype (fp8: round to nearest even; past the largest finite value e4m3fn

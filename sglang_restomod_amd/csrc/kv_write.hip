@@ -26,7 +26,7 @@ struct KvWriteArgs {
   const int64_t* loc;
   int64_t num_tokens;
   int hkv;
-  int chunk_shift;  // log2 of the 16-byte source chunks per row (head_dim / 8)
+  int chunks;       // 16-byte source chunks per row (head_dim / 8)
   void* k_cache;
   void* v_cache;
   int64_t cache_stride_row, cache_stride_head;  // elements of the cache dtype (bytes for fp8)
@@ -89,15 +89,19 @@ __device__ __forceinline__ void convert_chunk(const u32x4 in, float div, bool ap
   }
 }
 
-// Grid: x = blocks of 256 / (head_dim / 8) tokens, y = kv head, z = K (0) or V (1).
+// Grid: x = blocks of 256 / (head_dim / 8) tokens (threads past whole rows idle), y = kv
+// head, z = K (0) or V (1).
 template <int SRC, int DST>
 __global__ __launch_bounds__(256) void kv_write_kernel(const KvWriteArgs args) {
   const KvWriteArgs a = args;
   constexpr bool kFp8 = (DST == DT_E4M3 || DST == DT_E5M2);
   const int which = blockIdx.z;
   const int h = blockIdx.y;
-  const int part = threadIdx.x & ((1 << a.chunk_shift) - 1);
-  const int64_t t = ((int64_t)blockIdx.x << (8 - a.chunk_shift)) + (threadIdx.x >> a.chunk_shift);
+  const int per_block = 256 / a.chunks;
+  const int row = (int)threadIdx.x / a.chunks;
+  const int part = (int)threadIdx.x - row * a.chunks;
+  if (row >= per_block) return;
+  const int64_t t = (int64_t)blockIdx.x * per_block + row;
   if (t >= a.num_tokens) return;
   const int64_t slot = gptr(a.loc)[t];
   if (slot < 0 || slot >= a.num_slots) return;  // not a slot of this pool: nothing is written
@@ -140,8 +144,8 @@ extern "C" int ma_set_kv_buffer(const void* k, const void* v, int64_t src_stride
   if (src_dtype != DT_F16 && src_dtype != DT_BF16) return set_error(MA_EINVAL, "source dtype %d must be f16 or bf16", src_dtype);
   if (cache_dtype < DT_F16 || cache_dtype > DT_E5M2) return set_error(MA_EINVAL, "cache dtype %d unknown", cache_dtype);
   if (num_tokens < 0 || num_kv_heads <= 0 || num_slots < 0) return set_error(MA_EINVAL, "bad sizes");
-  if (head_dim < 8 || head_dim > 2048 || (head_dim & (head_dim - 1)))
-    return set_error(MA_EUNSUPPORTED, "head_dim %d must be a power of two in 8..2048", head_dim);
+  if (head_dim < 8 || head_dim > 2048 || (head_dim % 8))
+    return set_error(MA_EUNSUPPORTED, "head_dim %d must be a multiple of 8 in 8..2048", head_dim);
   if (apply_scale && !(k_scale > 0.f && v_scale > 0.f)) return set_error(MA_EINVAL, "scales must be positive");
   if (num_tokens == 0) return MA_OK;
   if (!k || !v || !loc || !k_cache || !v_cache) return set_error(MA_EINVAL, "null pointer argument");
@@ -157,13 +161,13 @@ extern "C" int ma_set_kv_buffer(const void* k, const void* v, int64_t src_stride
     return set_error(MA_EINVAL, "cache strides must keep rows %d-byte aligned", store_align);
   KvWriteArgs a{};
   a.k = k; a.v = v; a.src_stride_tok = src_stride_tok; a.src_stride_head = src_stride_head;
-  a.loc = loc; a.num_tokens = num_tokens; a.hkv = num_kv_heads; a.chunk_shift = __builtin_ctz(head_dim / 8);
+  a.loc = loc; a.num_tokens = num_tokens; a.hkv = num_kv_heads; a.chunks = head_dim / 8;
   a.k_cache = k_cache; a.v_cache = v_cache; a.cache_stride_row = cache_stride_row;
   a.cache_stride_head = cache_stride_head; a.num_slots = num_slots;
   a.apply_scale = apply_scale ? 1 : 0;
   a.k_div = apply_scale ? k_scale : 1.f;
   a.v_div = apply_scale ? v_scale : 1.f;
-  const int64_t per_block = 256 >> a.chunk_shift;  // tokens per block (head_dim <= 2048: at least 1)
+  const int64_t per_block = 256 / a.chunks;  // tokens per block (head_dim <= 2048: at least 1)
   const int64_t blocks = (num_tokens + per_block - 1) / per_block;
   if (blocks > 0x7fffffff || num_kv_heads > 65535) return set_error(MA_EINVAL, "too many tokens or heads");
   const dim3 grid((unsigned)blocks, (unsigned)num_kv_heads, 2);

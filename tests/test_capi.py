@@ -106,7 +106,8 @@ def _kvw_args(**over):
 @pytest.mark.parametrize("over,msg", [
     ({"sdt": 2}, "source dtype"),
     ({"cdt": 7}, "cache dtype"),
-    ({"dim": 100}, "power of two"),
+    ({"dim": 100}, "multiple of 8"),
+    ({"dim": 4096}, "multiple of 8"),
     ({"ks": 0.0}, "positive"),
     ({"k": (1 << 20) + 4}, "aligned"),
     ({"sst": 1001}, "source strides"),

@@ -111,10 +111,10 @@ def test_serving_sequence(kv_dtype):
 
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
-@pytest.mark.parametrize("hq,hkv,dim", [(8, 2, 64), (12, 2, 256)])
+@pytest.mark.parametrize("hq,hkv,dim", [(8, 2, 64), (12, 2, 256), (8, 2, 96), (16, 4, 512)])
 def test_serving_sequence_head_dims(kv_dtype, hq, hkv, dim):
     """The same sequence at head dims 64 and 256 (the latter with the 27B model's
-    per-GPU head counts)."""
+    per-GPU head counts), and at 96 and 512, which run on the any-head-dim kernel."""
     _serving_sequence(kv_dtype, hq, hkv, dim)
 
 

@@ -290,3 +290,62 @@ def test_paged_forward_with_the_reference_call_shape(gpu):
     assert lse2.shape == lse.shape
     _check_rows(q, k, v, lambda b, n: oracle.slots_from_page_table(t, b, n, 16), prefix, qsl, out2, rows_of,
                 128 ** -0.5, what="reference call shape, verify route")
+
+
+def test_bf16_v_outside_fp16_range():
+    """Extend runs PV in fp16: bf16 V is converted by round-toward-zero, which clamps values
+    beyond fp16's range to +-65504 (and keeps the rest exact, small values included).
+    The split-KV decode keeps bf16 V as it is. Both behaviours against the float64 oracle,
+    with errors relative to the largest |V| (P is normalised, so O is a convex mix of V)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(77)
+    B, hkv, G, D = 2, 2, 2, 128
+    prefix, ext = [40, 130], [24, 9]
+    seq = [p + e for p, e in zip(prefix, ext)]
+    pool = sum(seq) + 1
+    k = torch.randn(pool, hkv, D, generator=g).to(torch.bfloat16)
+    vf = torch.randn(pool, hkv, D, generator=g)
+    pick = torch.rand(pool, hkv, D, generator=g)
+    vf = torch.where(pick < 0.03, torch.sign(vf) * 1.0e5, vf)          # beyond fp16's range
+    vf = torch.where((pick >= 0.03) & (pick < 0.06), vf * 2.0e4, vf)     # large, inside it
+    vf = torch.where((pick >= 0.06) & (pick < 0.09), vf * 1.0e-6, vf)    # below fp16's normal range
+    v = vf.to(torch.bfloat16)
+    T = sum(ext)
+    q = torch.randn(T, hkv * G, D, generator=g).to(torch.bfloat16)
+    r2t = torch.zeros(B, max(seq), dtype=torch.int32)
+    off = 1
+    for b, n in enumerate(seq):
+        r2t[b, :n] = torch.arange(off, off + n, dtype=torch.int32)
+        off += n
+    qsl = [0, ext[0], ext[0] + ext[1]]
+    scale = D ** -0.5
+    slots = [r2t[b, :n].numpy().astype(np.int64) for b, n in enumerate(seq)]
+    kf = k.float().numpy().astype(np.float64)
+    v64 = v.float().numpy().astype(np.float64)
+    v_clamped = np.clip(v64, -65504.0, 65504.0)
+    ref_clamped = oracle.paged_attention(to_f64(q), kf, v_clamped, slots, qsl, prefix, seq, softmax_scale=scale)
+    ref_exact = oracle.paged_attention(to_f64(q), kf, v64, slots, qsl, prefix, seq, softmax_scale=scale)
+    vmax = float(np.abs(v64).max())
+    out = torch.empty(T, hkv * G, D, dtype=torch.float32, device=dev)
+    _ops().paged_extend_forward(q.to(dev), k.to(dev), v.to(dev), r2t.to(dev),
+                                torch.tensor(seq, dtype=torch.int32, device=dev),
+                                torch.tensor(qsl, dtype=torch.int32, device=dev),
+                                torch.tensor(prefix, dtype=torch.int32, device=dev), softmax_scale=scale, out=out)
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    err_clamped = float(np.abs(got - ref_clamped).max())
+    err_exact = float(np.abs(got - ref_exact).max())
+    print(f"[result] extend: max |err| vs clamped V {err_clamped:.3e}, vs exact V {err_exact:.3e} (max |V| {vmax:.3e})",
+          flush=True)
+    assert err_clamped <= 2e-3 * 65504.0, err_clamped
+    assert err_exact > 10 * err_clamped  # the clamp is what the kernel computes
+    # decode of each sequence's last token: bf16 V used as it is
+    qd = torch.stack([q[qsl[b + 1] - 1] for b in range(B)])
+    dec = torch.empty(B, hkv * G, D, dtype=torch.float32, device=dev)
+    _ops().grouped_decode_forward(qd.to(dev), k.to(dev), v.to(dev), r2t.to(dev),
+                                  torch.tensor(seq, dtype=torch.int32, device=dev), softmax_scale=scale, out=dec)
+    torch.cuda.synchronize()
+    ref_dec = np.stack([ref_exact[qsl[b + 1] - 1] for b in range(B)])
+    err_dec = float(np.abs(dec.double().cpu().numpy() - ref_dec).max())
+    print(f"[result] decode: max |err| vs exact V {err_dec:.3e}", flush=True)
+    assert err_dec <= 2e-3 * vmax, err_dec

@@ -112,3 +112,29 @@ def test_strided_rows_heads_and_out_of_pool_slots():
     written = set(int(x) for x in loc_np if 0 <= x < 100)
     others = [s for s in range(100) if s not in written]
     assert (_bits(kc, KW.E4M3)[others] == 0).all()
+
+
+@pytest.mark.parametrize("dim", [24, 96, 200, 520])
+@pytest.mark.parametrize("dst", [KW.E4M3, "bf16"])
+def test_head_dims_that_are_not_powers_of_two(dim, dst):
+    """Rows of any multiple of 8 (the any-head-dim layers' pools): bit-exact over the 16-bit
+    inputs that fill whole rows, untouched slots stay zero."""
+    gen = torch.Generator().manual_seed(dim)
+    heads = 2
+    n = ALL16.size // (heads * dim)
+    bits = ALL16[:n * heads * dim]
+    k = _src(bits, "bf16", heads=heads, dim=dim)
+    v = _src(bits[::-1].copy(), "bf16", heads=heads, dim=dim)
+    loc = torch.randperm(n + 50, generator=gen)[:n].to(DEV)
+    kc, vc = _cache(n + 50, heads, dim, dst), _cache(n + 50, heads, dim, dst)
+    _ops().set_kv_buffer(kc, vc, loc, k, v, 0.37, 2.5)
+    torch.cuda.synchronize()
+    loc_np = loc.cpu().numpy()
+    for cache, b, sc in ((kc, bits, 0.37), (vc, bits[::-1].copy(), 2.5)):
+        got = _bits(cache, dst)[loc_np].reshape(-1)
+        want = KW.quantize(b, "bf16", dst, sc if dst != "bf16" else None)
+        nan_in = np.isnan(KW.source_values(b, "bf16"))
+        bad = np.nonzero((got != want) & ~nan_in)[0]
+        assert bad.size == 0, (dim, dst, bad[:8])
+        untouched = np.setdiff1d(np.arange(n + 50), loc_np)
+        assert (_bits(cache, dst)[untouched] == 0).all()
