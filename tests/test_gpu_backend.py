@@ -142,11 +142,14 @@ def test_sliding_window_layer_through_swa_pool():
     del full
 
 
-def test_decode_in_a_hip_graph_replays_with_new_lengths():
+@pytest.mark.parametrize("HQ,HKV,D", [(HQ, HKV, D), (8, 2, 96), (16, 4, 512)])
+def test_decode_in_a_hip_graph_replays_with_new_lengths(HQ, HKV, D):
+    """At head dims 96 and 512 the decode runs on the any-head-dim kernel (no workspace)."""
+    print(f"[case] decode graph hq={HQ} hkv={HKV} d={D}", flush=True)
     gen = torch.Generator().manual_seed(3)
-    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=torch.bfloat16, pool_size=9000, max_reqs=8,
+    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, head_dim=D, kv_dtype=torch.bfloat16, pool_size=9000, max_reqs=8,
                        context_len=4096)
-    layer = _layer(torch.bfloat16)
+    layer = _layer(torch.bfloat16, HQ, HKV, D)
     be = _backend(eng)
     rows = [4, 1, 6, 0]
     for r, n in zip(rows, [700, 33, 1500, 260]):

@@ -1,7 +1,8 @@
 """ma_grouped_decode_noalloc through the C ABI against ma_grouped_decode on the same inputs:
 bit-identical outputs on two calls in a row, the second on a smaller batch (the static
-scratch keeps the first call's contents), at head dims 128 and 256 and with fp8 KV; a
-grid beyond the scratch is refused before any launch."""
+scratch keeps the first call's contents), at head dims 128, 256 and 512 (the last on the
+any-head-dim kernel, which uses no scratch) and with fp8 KV; a grid beyond the scratch is
+refused before any launch."""
 
 from __future__ import annotations
 
@@ -49,7 +50,8 @@ def _both(w, nwg):
     return want, got
 
 
-@pytest.mark.parametrize("index,kv_format,dim", [(1, "e4m3", 128), (3, "e5m2", 128), (5, "e4m3", 256)])
+@pytest.mark.parametrize("index,kv_format,dim", [(1, "e4m3", 128), (3, "e5m2", 128), (5, "e4m3", 256),
+                                                 (7, "e4m3", 512)])
 def test_noalloc_matches_the_workspace_entry_point(index, kv_format, dim):
     nwg = min(ops.splitkv_workgroups(DEV), _lib.MA_NOALLOC_MAX_WORKGROUPS)
     for call, (batch, scale) in enumerate(((24, 0.5), (5, 0.1))):  # the second call is smaller
