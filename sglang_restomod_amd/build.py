@@ -45,8 +45,19 @@ def common_flags() -> list[str]:
     ]
 
 
+# Flags of single sources. paged_any's kernels hold their MFMA accumulators in ordinary
+# VGPRs: with them in AGPRs, the online-softmax rescale (VALU, which cannot address AGPRs)
+# made the register allocator copy the whole output block between the two register files
+# on every key tile.
+SOURCE_FLAGS = {"paged_any": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
+def _flags(src: Path, extra: list[str]) -> list[str]:
+    return [*common_flags(), *SOURCE_FLAGS.get(src.stem, []), *extra]
+
+
 def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
-    cmd = [hipcc(), *common_flags(), *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *_flags(src, extra), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
@@ -56,7 +67,7 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
 def _assembly(src: Path, extra: list[str]) -> Path:
     """Device assembly of `src` (for the static checks)."""
     asm = CSRC / "_build" / (src.stem + ".s")
-    cmd = [hipcc(), *common_flags(), *extra, "-S", "--cuda-device-only", str(src), "-o", str(asm)]
+    cmd = [hipcc(), *_flags(src, extra), "-S", "--cuda-device-only", str(src), "-o", str(asm)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"assembly generation failed: {' '.join(cmd)}\n{proc.stderr}")

@@ -236,18 +236,35 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       return s;
     };
     // scores of tile i from a K tile in LDS (shared mode)
+    // The operand reads run one batch of kFB steps ahead of the MFMAs; the scheduling
+    // barriers keep the compiler from sinking each read down to its MFMA, which left every
+    // MFMA waiting out a full LDS latency.
     auto scores_lds = [&](uint32_t kt) __attribute__((always_inline)) -> f32x4 {
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
       const uint32_t ka0 = kt + c * kRowK + j * 16;
+      constexpr int kFB = KK < 4 ? KK : 4;  // QK steps per batch
+      constexpr int kNB = KK / kFB;
+      u32x4 kf[2][kFB], qf[2][kFB];
+      auto fetch = [&](int bb, int sl) __attribute__((always_inline)) {
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const u32x4 kf = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(ka0 + kk * 64));
-        if constexpr (kQLds) {
-          const u32x4 qf = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(qa + kk * 64));
-          s = mfma16t<QBF16>(kf, qf, s);
-        } else {
-          s = mfma16t<QBF16>(kf, qv[kk], s);
+        for (int x = 0; x < kFB; ++x) {
+          const int kk = bb * kFB + x;
+          kf[sl][x] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(ka0 + kk * 64));
+          if constexpr (kQLds)
+            qf[sl][x] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(qa + kk * 64));
         }
+      };
+      fetch(0, 0);
+#pragma unroll
+      for (int bb = 0; bb < kNB; ++bb) {
+        if (bb + 1 < kNB) fetch(bb + 1, (bb + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int x = 0; x < kFB; ++x) {
+          if constexpr (kQLds) s = mfma16t<QBF16>(kf[bb & 1][x], qf[bb & 1][x], s);
+          else s = mfma16t<QBF16>(kf[bb & 1][x], qv[bb * kFB + x], s);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
       return s;
     };
@@ -276,15 +293,28 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(s[e] * a.scale_log2 - msc);
       lsum += (p[0] + p[1]) + (p[2] + p[3]);
       const u32x2 pk = u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
-      // O^T[d][row] += V^T[d][key] P^T[key][row], 16 dims per step
+      // O^T[d][row] += V^T[d][key] P^T[key][row], 16 dims per step; the transposed V reads
+      // run one batch of kVB steps ahead, as in the scores
       const uint32_t vb = vt + (4 * j + (c >> 2)) * kRowL + (c & 3) * 8;
+      constexpr int kVB = DB < 8 ? DB : 8;
+      constexpr int kVNB = DB / kVB;
+      u32x2 vf[2][kVB];
+      auto vfetch = [&](int bb, int sl) __attribute__((always_inline)) {
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const uint32_t addr = vb + db * 32;
-        const u32x2 va = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)(uintptr_t)addr));
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, va), __builtin_bit_cast(f16x4, pk),
-                                                      o[db], 0, 0, 0);
+        for (int x = 0; x < kVB; ++x)
+          vf[sl][x] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(uintptr_t)(vb + (bb * kVB + x) * 32)));
+      };
+      vfetch(0, 0);
+#pragma unroll
+      for (int bb = 0; bb < kVNB; ++bb) {
+        if (bb + 1 < kVNB) vfetch(bb + 1, (bb + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int x = 0; x < kVB; ++x)
+          o[bb * kVB + x] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+              __builtin_bit_cast(f16x4, vf[bb & 1][x]), __builtin_bit_cast(f16x4, pk), o[bb * kVB + x], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
     };
 
@@ -315,7 +345,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
 #pragma unroll
         for (int x = 0; x < kUW; ++x) {
           const int u = (int)threadIdx.x + kAnyWaves * 64 * x;
-          if (u < kTileUnits) {
+          if (kTileUnits % (kAnyWaves * 64) == 0 || u < kTileUnits) {
             const int key = u / kUnits;
             const int q = u - key * kUnits;
             u32x4 kh, vh;
@@ -352,8 +382,11 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       __syncthreads();
       auto tile_step = [&](int i, u32x4 (&kn)[kUW], VRaw (&vn)[kUW]) __attribute__((always_inline)) {
         write_units(stage(i + 1), kn, vn);       // tile i+1, buffer (i+1) % 2
+        // the next page lookup goes out before the unit loads, so the step that uses it
+        // waits for it alone, not for the units behind it
+        const int pn = page_load(i + 4);
         load_units(slot_of(i + 3, pg), kn, vn);  // tile i+3 into the buffer just written
-        pg = page_load(i + 4);
+        pg = pn;
         finish(i, scores_lds(stage(i)), stage(i) + kKTile);
         __syncthreads();
       };
