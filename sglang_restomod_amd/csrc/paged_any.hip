@@ -37,8 +37,21 @@ struct AnyVRaw<true> {
   typedef u32x2 type;
 };
 
-template <int DP, bool QBF16, int KV>
-__global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(const AnyArgs args) {
+// the mode of one call of the row routine, fixed at compile time
+template <bool SHARED>
+struct AnyMode {
+  static constexpr bool shared = SHARED;
+};
+
+// SHARED: the extend kernel (work list, shared K/V ring); otherwise decode and verify
+// (split keys). Two workgroups share a CU where the registers allow it.
+template <bool SHARED, int DP>
+constexpr int any_wg_per_cu() {
+  return (DP >= 512 || (DP >= 256 && !SHARED)) ? 1 : 2;
+}
+
+template <int DP, bool QBF16, int KV, bool SHARED>
+__global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void any_kernel(const AnyArgs args) {
   const AnyArgs a = args;  // local copy: the lambdas capture by reference
   constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
   constexpr int KK = DP / 32;                   // QK MFMA steps
@@ -60,22 +73,31 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
   constexpr int kQRow = DP * 2 + 16;
   constexpr int kVBlock = kAnyKeys * kRowL;            // one wave's V rows
   constexpr int kQBlock = kQLds ? kAnyRows * kQRow : 0;  // one wave's Q rows
-  constexpr int kSmem = kAnyWaves * (kVBlock + kQBlock);
-  // When the four waves split one row block's keys, their partial O meet in the same
-  // memory after the loop, kBPR 16-column blocks (1 KiB per wave each) at a time.
-  constexpr int kBPR = (DB * kAnyWaves * 1024 <= kSmem) ? DB
-                       : (DB / 2 * kAnyWaves * 1024 <= kSmem) ? DB / 2
-                       : (DB / 4 * kAnyWaves * 1024 <= kSmem) ? DB / 4 : DB / 8;
-  static_assert(kBPR >= 1 && kBPR * kAnyWaves * 1024 <= kSmem, "merge rounds fit the V/Q memory");
   // Extend rows: the four waves own 64 consecutive rows of one sequence and kv head and
-  // share every K/V tile through a two-stage LDS ring (16-bit K rows padded by 16 bytes,
-  // fp16 V rows as above), loaded once per workgroup; kUW 16-byte units per thread.
+  // share every K/V tile through a three-stage LDS ring (16-bit K rows padded by 16 bytes,
+  // fp16 V rows as above), loaded once per workgroup; kUW 16-byte units per thread. Each
+  // wave computes the scores and softmax of its own 16 rows, and O for a quarter of the
+  // dims (kCB 16-dim blocks) of all 64 rows: P, the rescale factors and their flags pass
+  // through the exchange memory behind the ring (two tiles deep).
   constexpr int kRowK = DP * 2 + 16;
   constexpr int kKTile = kAnyKeys * kRowK;
   constexpr int kStageB = kKTile + kVBlock;
   constexpr int kTileUnits = kAnyKeys * kUnits;  // 16-byte units of one K (or V) tile
   constexpr int kUW = kTileUnits >= kAnyWaves * 64 ? kTileUnits / (kAnyWaves * 64) : 1;
-  static_assert(2 * kStageB <= kAnyWaves * kVBlock, "the ring fits the per-wave V memory it replaces");
+  constexpr int kCB = DB / kAnyWaves;
+  static_assert(kCB >= 1 && DB % kAnyWaves == 0, "whole dim blocks per wave");
+  constexpr int kXP = 0;                                   // P: [tile & 1][wave][lane] u32x2
+  constexpr int kXA = kXP + 2 * kAnyWaves * 64 * 8;        // factors: [tile & 1][wave][row] f32
+  constexpr int kXF = kXA + 2 * kAnyWaves * kAnyRows * 4;  // flags: [tile & 1][wave] u32
+  constexpr int kXBytes = kXF + 2 * kAnyWaves * 4;
+  constexpr int kRing = 3 * kStageB;
+  constexpr int kSmem = SHARED ? kRing + kXBytes : kAnyWaves * (kVBlock + kQBlock);
+  // When the four waves split one row block's keys, their partial O meet in the same
+  // memory after the loop, kBPR 16-column blocks (1 KiB per wave each) at a time.
+  constexpr int kBPR = (DB * kAnyWaves * 1024 <= kSmem) ? DB
+                       : (DB / 2 * kAnyWaves * 1024 <= kSmem) ? DB / 2
+                       : (DB / 4 * kAnyWaves * 1024 <= kSmem) ? DB / 4 : DB / 8;
+  static_assert(kBPR >= 1 && kBPR * kAnyWaves * 1024 <= kSmem, "merge rounds fit the kernel's LDS");
   __shared__ __attribute__((aligned(256))) unsigned char smem[kSmem];
   __shared__ float mrow[kAnyWaves][2][kAnyRows];  // each wave's row max and row sum of p
 
@@ -99,12 +121,12 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
   const int64_t row_bytes = a.kv_stride_row * kElt;
   const int page_mask = (1 << a.tt.page_shift) - 1;
 
-  // One wave's 16 rows r0 .. r0 + 15 of sequence b, kv head h. split < 0: the workgroup's
-  // four waves own consecutive row blocks (rows r0 - 16 * wave ..) and walk the keys any
-  // of them sees together, sharing each K/V tile. split >= 0: the four waves own the same
-  // row block and take quarter `split` of its key tiles each, merging at the end.
-  auto rows = [&](int b, int h, int r0, int split) __attribute__((always_inline)) {
-    const bool shared = split < 0;
+  // One wave's 16 rows r0 .. r0 + 15 of sequence b, kv head h. Shared mode: the
+  // workgroup's four waves own consecutive row blocks (rows r0 - 16 * wave ..) and walk the
+  // keys any of them sees together, sharing each K/V tile. Otherwise the four waves own the
+  // same row block and take quarter `split` of its key tiles each, merging at the end.
+  auto rows = [&](auto mode, int b, int h, int r0, int split) __attribute__((always_inline)) {
+    constexpr bool shared = decltype(mode)::shared;
     const int rg0 = shared ? r0 - wave * kAnyRows : r0;  // first row of the workgroup's rows
     const int rgn = shared ? kAnyWaves * kAnyRows : kAnyRows;
     int tok0, ntok;
@@ -130,7 +152,8 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
     const int qpos = prefix + t;
     const int lo_r = (real && a.window >= 0) ? max(0, qpos - a.window) : 0;
     const int hi_r = real ? (a.causal ? min(seq, qpos + 1) : seq) : 0;
-    u32x4 qv[kQLds ? 1 : KK];
+    constexpr bool kQInLds = kQLds && !shared;  // shared mode keeps Q in registers
+    u32x4 qv[kQInLds ? 1 : KK];
     const uint32_t qa = q_base + c * kQRow + j * 16;
     {
       const uint16_t MA_GLOBAL* qp = gptr(reinterpret_cast<const uint16_t*>(a.q)) +
@@ -140,7 +163,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       for (int kk = 0; kk < KK; ++kk) {
         const int d0 = shared ? kk * 32 + j * 8 : qdim(kk);
         const u32x4 qf = (real && d0 < D) ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + d0) : u32x4{0, 0, 0, 0};
-        if constexpr (kQLds) *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(qa + kk * 64)) = qf;
+        if constexpr (kQInLds) *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(qa + kk * 64)) = qf;
         else qv[kk] = qf;
       }
     }
@@ -226,7 +249,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       } else {
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-          if constexpr (kQLds) {
+          if constexpr (kQInLds) {
             const u32x4 qf = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(qa + kk * 64));
             s = mfma16t<QBF16>(kr[kk], qf, s);
           } else
@@ -235,24 +258,20 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       }
       return s;
     };
-    // scores of tile i from a K tile in LDS (shared mode)
+    // scores of tile i from a K tile in LDS (shared mode, Q in registers)
     // The operand reads run one batch of kFB steps ahead of the MFMAs; the scheduling
     // barriers keep the compiler from sinking each read down to its MFMA, which left every
     // MFMA waiting out a full LDS latency.
     auto scores_lds = [&](uint32_t kt) __attribute__((always_inline)) -> f32x4 {
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 s2[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};  // two MFMA chains
       const uint32_t ka0 = kt + c * kRowK + j * 16;
       constexpr int kFB = KK < 4 ? KK : 4;  // QK steps per batch
       constexpr int kNB = KK / kFB;
-      u32x4 kf[2][kFB], qf[2][kFB];
+      u32x4 kf[2][kFB];
       auto fetch = [&](int bb, int sl) __attribute__((always_inline)) {
 #pragma unroll
-        for (int x = 0; x < kFB; ++x) {
-          const int kk = bb * kFB + x;
-          kf[sl][x] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(ka0 + kk * 64));
-          if constexpr (kQLds)
-            qf[sl][x] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(qa + kk * 64));
-        }
+        for (int x = 0; x < kFB; ++x)
+          kf[sl][x] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(ka0 + (bb * kFB + x) * 64));
       };
       fetch(0, 0);
 #pragma unroll
@@ -260,31 +279,30 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
         if (bb + 1 < kNB) fetch(bb + 1, (bb + 1) & 1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int x = 0; x < kFB; ++x) {
-          if constexpr (kQLds) s = mfma16t<QBF16>(kf[bb & 1][x], qf[bb & 1][x], s);
-          else s = mfma16t<QBF16>(kf[bb & 1][x], qv[bb * kFB + x], s);
-        }
+        for (int x = 0; x < kFB; ++x) s2[x & 1] = mfma16t<QBF16>(kf[bb & 1][x], qv[bb * kFB + x], s2[x & 1]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      return s;
+      return s2[0] + s2[1];
     };
-    // softmax and PV of tile i (its V in LDS at vt)
-    auto finish = [&](int i, f32x4 s, uint32_t vt) __attribute__((always_inline)) {
+    // Online softmax of tile i's scores (lane (c, j): keys 4j .. 4j + 3 of row c). Returns
+    // p in fp16; `moved` (the same in every lane) says whether some row's exponent base
+    // moved, and then `alpha` is the factor the row's earlier O takes (1 for the others).
+    // The base moves only when a row's max grew by more than 2^kLazyRescale in p.
+    auto softmax = [&](int i, f32x4 s, float& alpha, bool& moved) __attribute__((always_inline)) -> u32x2 {
       const int kb0 = key_lo + i * kAnyKeys + 4 * j;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (kb0 + e < lo_r || kb0 + e >= hi_r) s[e] = -INFINITY;
       float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      // the exponent base moves only when some row's max grew by more than 2^kLazyRescale in p
-      if (__builtin_amdgcn_ballot_w64((mx - m_run) * a.scale_log2 > kLazyRescale)) {
+      alpha = 1.f;
+      moved = __builtin_amdgcn_ballot_w64((mx - m_run) * a.scale_log2 > kLazyRescale) != 0;
+      if (moved) {
         mx = fmaxf(mx, shfl_xor_f(mx, 16));
         mx = fmaxf(mx, shfl_xor_f(mx, 32));
         const float m_new = fmaxf(m_run, mx);
         const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * a.scale_log2);
+        alpha = __builtin_amdgcn_exp2f((m_run - m_use) * a.scale_log2);
         m_run = m_new;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[db] *= alpha;
         lsum *= alpha;
       }
       const float msc = (m_run == -INFINITY ? 0.f : m_run) * a.scale_log2;
@@ -292,7 +310,17 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(s[e] * a.scale_log2 - msc);
       lsum += (p[0] + p[1]) + (p[2] + p[3]);
-      const u32x2 pk = u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
+      return u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
+    };
+    // softmax and PV of tile i in split mode (its V in this wave's LDS rows at vt)
+    auto finish = [&](int i, f32x4 s, uint32_t vt) __attribute__((always_inline)) {
+      float alpha;
+      bool moved;
+      const u32x2 pk = softmax(i, s, alpha, moved);
+      if (moved) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db] *= alpha;
+      }
       // O^T[d][row] += V^T[d][key] P^T[key][row], 16 dims per step; the transposed V reads
       // run one batch of kVB steps ahead, as in the scores
       const uint32_t vb = vt + (4 * j + (c >> 2)) * kRowL + (c & 3) * 8;
@@ -318,11 +346,19 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
       }
     };
 
+    // LDS words of the shared mode's exchange memory
+    const uint32_t xbase = smem_base + kRing;
+    auto xp = [&](int i, int w) -> uint32_t { return xbase + kXP + ((i & 1) * kAnyWaves + w) * 512; };
+    auto xa = [&](int i, int w) -> uint32_t { return xbase + kXA + ((i & 1) * kAnyWaves + w) * (kAnyRows * 4); };
+    auto xf = [&](int i) -> uint32_t { return xbase + kXF + (i & 1) * (kAnyWaves * 4); };
     if (shared && nt > 0) {
       // The workgroup's tile ring. Step i writes tile i+1 (loaded during step i-1) to stage
-      // (i+1) % 2, loads tile i+2, computes tile i from stage i % 2, then meets the other
-      // waves: the barrier publishes stage (i+1) % 2 and retires stage i % 2. Tiles past
-      // the last are the last again (key positions clamp), every load is unconditional.
+      // (i+1) % 3, loads tile i+3, computes the scores and softmax of tile i from stage
+      // i % 3 and publishes P, then meets the other waves, then accumulates PV for its
+      // dims from every wave's P. The barrier of step i publishes stage (i+1) % 3 and tile
+      // i's P; stage (i+2) % 3, which step i+1 writes, was last read before the barrier
+      // of step i-1, and so were the exchange words of tile i-2. Tiles past the last are
+      // the last again (key positions clamp), every load is unconditional.
       u32x4 kraw0[kUW], kraw1[kUW];
       VRaw vraw0[kUW], vraw1[kUW];
       auto load_units = [&](int myslot, u32x4 (&kraw)[kUW], VRaw (&vraw)[kUW]) __attribute__((always_inline)) {
@@ -368,17 +404,19 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
           }
         }
       };
-      auto stage = [&](int i) -> uint32_t { return smem_base + (i & 1) * kStageB; };
+      auto stage = [&](int i) -> uint32_t { return smem_base + (uint32_t)(i % 3) * kStageB; };
       // tile t's raw units live in buffer t % 2 from the step that loads them (t - 3) to
       // the step that writes them to LDS (t - 1): two tiles' compute to land in
-      int pg = page_load(0);
-      load_units(slot_of(0, pg), kraw0, vraw0);
-      pg = page_load(1);
-      load_units(slot_of(1, pg), kraw1, vraw1);
-      pg = page_load(2);
+      // (the prologue issues its loads in the steps' order, each page lookup ahead of the
+      // units before it, so the loop starts with the load counts its back edge brings)
+      const int pg0 = page_load(0);
+      const int pg1 = page_load(1);
+      load_units(slot_of(0, pg0), kraw0, vraw0);
+      const int pg2 = page_load(2);
+      load_units(slot_of(1, pg1), kraw1, vraw1);
       write_units(stage(0), kraw0, vraw0);
-      load_units(slot_of(2, pg), kraw0, vraw0);
-      pg = page_load(3);
+      int pg = page_load(3);
+      load_units(slot_of(2, pg2), kraw0, vraw0);
       __syncthreads();
       auto tile_step = [&](int i, u32x4 (&kn)[kUW], VRaw (&vn)[kUW]) __attribute__((always_inline)) {
         write_units(stage(i + 1), kn, vn);       // tile i+1, buffer (i+1) % 2
@@ -387,14 +425,51 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
         const int pn = page_load(i + 4);
         load_units(slot_of(i + 3, pg), kn, vn);  // tile i+3 into the buffer just written
         pg = pn;
-        finish(i, scores_lds(stage(i)), stage(i) + kKTile);
+        float alpha;
+        bool moved;
+        const u32x2 pk = softmax(i, scores_lds(stage(i)), alpha, moved);
+        *reinterpret_cast<__attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, wave) + lane * 8)) = pk;
+        if (lane == 0) *reinterpret_cast<__attribute__((address_space(3))) uint32_t*>((uintptr_t)(xf(i) + wave * 4)) = moved;
+        if (moved && j == 0) *reinterpret_cast<__attribute__((address_space(3))) float*>((uintptr_t)(xa(i, wave) + c * 4)) = alpha;
+        // O^T[d][row] += V^T[d][key] P^T[key][row] for this wave's kCB dim blocks and the
+        // four row blocks: each V^T fragment is read once (before the barrier: its stage was
+        // published by the previous one) and meets four P fragments
+        const uint32_t vb = stage(i) + kKTile + (4 * j + (c >> 2)) * kRowL + (c & 3) * 8 + wave * kCB * 32;
+        u32x2 vf[kCB], pf[kAnyWaves];
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb)
+          vf[cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(uintptr_t)(vb + cb * 32)));
         __syncthreads();
+        const u32x4 fl = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)xf(i));
+#pragma unroll
+        for (int rb = 0; rb < kAnyWaves; ++rb)
+          pf[rb] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, rb) + lane * 8));
+        // the rows whose exponent base moved take their factor in this wave's dims
+#pragma unroll
+        for (int rb = 0; rb < kAnyWaves; ++rb) {
+          if (__builtin_amdgcn_readfirstlane(fl[rb])) {
+            const float al = *reinterpret_cast<const __attribute__((address_space(3))) float*>((uintptr_t)(xa(i, rb) + c * 4));
+#pragma unroll
+            for (int cb = 0; cb < kCB; ++cb) o[rb * kCB + cb] *= al;
+          }
+        }
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+          for (int rb = 0; rb < kAnyWaves; ++rb)
+            o[rb * kCB + cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                __builtin_bit_cast(f16x4, vf[cb]), __builtin_bit_cast(f16x4, pf[rb]), o[rb * kCB + cb], 0, 0, 0);
       };
+      // the odd last step runs after the loop, so the loop's back edge is its only path
+      // to the next pass and the compiler's load counts stay exact there
+      int i = 0;
 #pragma unroll 1
-      for (int i = 0; i < nt; i += 2) {
+      for (; i + 1 < nt; i += 2) {
         tile_step(i, kraw1, vraw1);
-        if (i + 1 < nt) tile_step(i + 1, kraw0, vraw0);
+        tile_step(i + 1, kraw0, vraw0);
       }
+      if (i < nt) tile_step(i, kraw1, vraw1);
     }
     if (!shared && i_hi > i_lo) {
       // Step i issues the slot lookup of tile i+2, writes tile i's V to LDS and refills the
@@ -426,33 +501,52 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
         finish(i, s, lds_base);
         page1 = page2;
       };
+      int i = i_lo;
 #pragma unroll 1
-      for (int i = i_lo; i < i_hi; i += 2) {
+      for (; i + 1 < i_hi; i += 2) {
         if constexpr (kTwoK) {
           step(i, ka, kb);
-          if (i + 1 < i_hi) step(i + 1, kb, ka);
+          step(i + 1, kb, ka);
         } else {
           step(i, ka, ka);
-          if (i + 1 < i_hi) step(i + 1, ka, ka);
+          step(i + 1, ka, ka);
         }
       }
+      if (i < i_hi) step(i, ka, kTwoK ? kb : ka);
     }
 
-    // normalise and store this lane's row: dims db * 16 + 4j .. + 3
+    // normalise and store: row sums first
     float lt = lsum + shfl_xor_f(lsum, 16);
     lt += shfl_xor_f(lt, 32);
-    const int64_t off = (int64_t)(tok0 + t) * a.out_stride_tok + (int64_t)(h * G + g) * a.out_stride_head;
-    if (shared) {
-      if (real) {
-        const float inv = (lt > 0.f) ? a.v_scale / lt : 0.f;
+    if constexpr (shared) {
+      // Each row's owner publishes its sum of p (in the factor words of tile nt, whose last
+      // readers were done before the barrier of step nt-1); this wave then stores its dims
+      // of all 64 rows. The second barrier keeps the words until every wave has read them.
+      if (j == 0) *reinterpret_cast<__attribute__((address_space(3))) float*>((uintptr_t)(xa(nt, wave) + c * 4)) = lt;
+      __syncthreads();
+      float ls[kAnyWaves];
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          if (db * 16 >= D) break;
-          store_out4<QBF16>(a.out, off + db * 16 + 4 * j, o[db], inv, a.out_f32);
+      for (int rb = 0; rb < kAnyWaves; ++rb)
+        ls[rb] = *reinterpret_cast<const __attribute__((address_space(3))) float*>((uintptr_t)(xa(nt, rb) + c * 4));
+      __syncthreads();
+#pragma unroll
+      for (int rb = 0; rb < kAnyWaves; ++rb) {
+        const int rr = rg0 + rb * kAnyRows + c;
+        const int tr = rr / G;
+        if (tr < ntok) {
+          const int gr = rr - tr * G;
+          const int64_t offr = (int64_t)(tok0 + tr) * a.out_stride_tok + (int64_t)(h * G + gr) * a.out_stride_head;
+          const float inv = (ls[rb] > 0.f) ? a.v_scale / ls[rb] : 0.f;
+#pragma unroll
+          for (int cb = 0; cb < kCB; ++cb) {
+            const int d0 = (wave * kCB + cb) * 16;
+            if (d0 < D) store_out4<QBF16>(a.out, offr + d0 + 4 * j, o[rb * kCB + cb], inv, a.out_f32);
+          }
         }
       }
       return;
     }
+    const int64_t off = (int64_t)(tok0 + t) * a.out_stride_tok + (int64_t)(h * G + g) * a.out_stride_head;
     // merge of the four quarters: each O and row sum is relative to its wave's exponent
     // base (its row max, 0 when it saw no key), rescaled to the largest
     if (j == 0) {
@@ -492,7 +586,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
     }
   };
 
-  if (a.items) {
+  if constexpr (SHARED) {
     // one 128-row work-list entry per workgroup and kv head, in two passes of 64 rows
     const int entry = (int)blockIdx.x / a.hkv;
     const int h = (int)blockIdx.x - entry * a.hkv;
@@ -502,7 +596,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
     const int rt = (int)(work >> 32);
 #pragma unroll 1
     for (int pass = 0; pass < kAnyPlanRows / (kAnyWaves * kAnyRows); ++pass)
-      rows(b, h, rt * kAnyPlanRows + pass * (kAnyWaves * kAnyRows) + wave * kAnyRows, -1);
+      rows(AnyMode<true>{}, b, h, rt * kAnyPlanRows + pass * (kAnyWaves * kAnyRows) + wave * kAnyRows, -1);
   } else {
     // decode and verify: workgroup item = (kv head, 16-row block, sequence), kv head
     // fastest; its four waves take the four quarters of the rows' key tiles. A sequence
@@ -517,19 +611,24 @@ __global__ __launch_bounds__(kAnyWaves * 64, DP >= 256 ? 1 : 2) void any_kernel(
     if (a.qsl) rows_b = clamp_query_rows(cptr(a.qsl)[b], cptr(a.qsl)[b + 1], a.num_tokens).ntok * a.group;
     else rows_b = (b < a.num_tokens ? 1 : 0) * a.group;
 #pragma unroll 1
-    for (int r0 = rb * kAnyRows; r0 < rows_b; r0 += a.row_blocks * kAnyRows) rows(b, h, r0, wave);
+    for (int r0 = rb * kAnyRows; r0 < rows_b; r0 += a.row_blocks * kAnyRows) rows(AnyMode<false>{}, b, h, r0, wave);
   }
+}
+
+template <int DP, bool QBF16, bool SHARED>
+static hipError_t launch_any_m(int kv, dim3 grid, hipStream_t st, const AnyArgs& a) {
+  if (kv == DT_E4M3)
+    hipLaunchKernelGGL((any_kernel<DP, QBF16, DT_E4M3, SHARED>), grid, dim3(kAnyWaves * 64), 0, st, a);
+  else if (kv == DT_E5M2)
+    hipLaunchKernelGGL((any_kernel<DP, QBF16, DT_E5M2, SHARED>), grid, dim3(kAnyWaves * 64), 0, st, a);
+  else
+    hipLaunchKernelGGL((any_kernel<DP, QBF16, QBF16 ? DT_BF16 : DT_F16, SHARED>), grid, dim3(kAnyWaves * 64), 0, st, a);
+  return hipGetLastError();
 }
 
 template <int DP, bool QBF16>
 static hipError_t launch_any_q(int kv, dim3 grid, hipStream_t st, const AnyArgs& a) {
-  if (kv == DT_E4M3)
-    hipLaunchKernelGGL((any_kernel<DP, QBF16, DT_E4M3>), grid, dim3(kAnyWaves * 64), 0, st, a);
-  else if (kv == DT_E5M2)
-    hipLaunchKernelGGL((any_kernel<DP, QBF16, DT_E5M2>), grid, dim3(kAnyWaves * 64), 0, st, a);
-  else
-    hipLaunchKernelGGL((any_kernel<DP, QBF16, QBF16 ? DT_BF16 : DT_F16>), grid, dim3(kAnyWaves * 64), 0, st, a);
-  return hipGetLastError();
+  return a.items ? launch_any_m<DP, QBF16, true>(kv, grid, st, a) : launch_any_m<DP, QBF16, false>(kv, grid, st, a);
 }
 
 template <int DP>
