@@ -27,6 +27,8 @@ struct KvWriteArgs {
   int64_t num_tokens;
   int hkv;
   int chunks;       // 16-byte source chunks per row (head_dim / 8)
+  int chunk_shift;  // log2(chunks) when chunks is a power of two, else -1
+  int per_block;    // whole rows per 256-thread block
   void* k_cache;
   void* v_cache;
   int64_t cache_stride_row, cache_stride_head;  // elements of the cache dtype (bytes for fp8)
@@ -97,9 +99,15 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const KvWriteArgs args) {
   constexpr bool kFp8 = (DST == DT_E4M3 || DST == DT_E5M2);
   const int which = blockIdx.z;
   const int h = blockIdx.y;
-  const int per_block = 256 / a.chunks;
-  const int row = (int)threadIdx.x / a.chunks;
-  const int part = (int)threadIdx.x - row * a.chunks;
+  const int per_block = a.per_block;
+  int row, part;
+  if (a.chunk_shift >= 0) {  // the common head dims: shifts, not a division
+    row = (int)threadIdx.x >> a.chunk_shift;
+    part = (int)threadIdx.x & (a.chunks - 1);
+  } else {
+    row = (int)threadIdx.x / a.chunks;
+    part = (int)threadIdx.x - row * a.chunks;
+  }
   if (row >= per_block) return;
   const int64_t t = (int64_t)blockIdx.x * per_block + row;
   if (t >= a.num_tokens) return;
@@ -168,6 +176,8 @@ extern "C" int ma_set_kv_buffer(const void* k, const void* v, int64_t src_stride
   a.k_div = apply_scale ? k_scale : 1.f;
   a.v_div = apply_scale ? v_scale : 1.f;
   const int64_t per_block = 256 / a.chunks;  // tokens per block (head_dim <= 2048: at least 1)
+  a.per_block = (int)per_block;
+  a.chunk_shift = (a.chunks & (a.chunks - 1)) ? -1 : __builtin_ctz((unsigned)a.chunks);
   const int64_t blocks = (num_tokens + per_block - 1) / per_block;
   if (blocks > 0x7fffffff || num_kv_heads > 65535) return set_error(MA_EINVAL, "too many tokens or heads");
   const dim3 grid((unsigned)blocks, (unsigned)num_kv_heads, 2);
