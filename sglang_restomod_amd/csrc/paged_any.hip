@@ -74,20 +74,23 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
   constexpr int kVBlock = kAnyKeys * kRowL;            // one wave's V rows
   constexpr int kQBlock = kQLds ? kAnyRows * kQRow : 0;  // one wave's Q rows
   // Extend rows: the four waves own 64 consecutive rows of one sequence and kv head and
-  // share every K/V tile through a three-stage LDS ring (16-bit K rows padded by 16 bytes,
-  // fp16 V rows as above), loaded once per workgroup; kUW 16-byte units per thread. Each
-  // wave computes the scores and softmax of its own 16 rows, and O for a quarter of the
-  // dims (kCB 16-dim blocks) of all 64 rows: P, the rescale factors and their flags pass
-  // through the exchange memory behind the ring (two tiles deep).
+  // share every K/V tile (kKT keys: 32 up to 128 dims, else 16) through a three-stage LDS
+  // ring (16-bit K rows padded by 16 bytes, fp16 V rows as above), loaded once per
+  // workgroup; kUW 16-byte units per thread. Each wave computes the scores and softmax of
+  // its own 16 rows, and O for a quarter of the dims (kCB 16-dim blocks) of all 64 rows:
+  // P, the rescale factors and their flags pass through the exchange memory behind the
+  // ring (two tiles deep). Decode and verify tiles have 16 keys.
+  constexpr int kKT = (SHARED && DP <= 128) ? 2 * kAnyKeys : kAnyKeys;
+  constexpr int kNS = kKT / kAnyKeys;  // 16-key score blocks per tile
   constexpr int kRowK = DP * 2 + 16;
-  constexpr int kKTile = kAnyKeys * kRowK;
-  constexpr int kStageB = kKTile + kVBlock;
-  constexpr int kTileUnits = kAnyKeys * kUnits;  // 16-byte units of one K (or V) tile
+  constexpr int kKTile = kKT * kRowK;
+  constexpr int kStageB = kKTile + kKT * kRowL;
+  constexpr int kTileUnits = kKT * kUnits;  // 16-byte units of one K (or V) tile
   constexpr int kUW = kTileUnits >= kAnyWaves * 64 ? kTileUnits / (kAnyWaves * 64) : 1;
   constexpr int kCB = DB / kAnyWaves;
   static_assert(kCB >= 1 && DB % kAnyWaves == 0, "whole dim blocks per wave");
-  constexpr int kXP = 0;                                   // P: [tile & 1][wave][lane] u32x2
-  constexpr int kXA = kXP + 2 * kAnyWaves * 64 * 8;        // factors: [tile & 1][wave][row] f32
+  constexpr int kXP = 0;                                   // P: [tile & 1][wave][block][lane] u32x2
+  constexpr int kXA = kXP + 2 * kAnyWaves * kNS * 64 * 8;  // factors: [tile & 1][wave][row] f32
   constexpr int kXF = kXA + 2 * kAnyWaves * kAnyRows * 4;  // flags: [tile & 1][wave] u32
   constexpr int kXBytes = kXF + 2 * kAnyWaves * 4;
   constexpr int kRing = 3 * kStageB;
@@ -172,7 +175,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
     const int t_last = min(ntok - 1, (rg0 + rgn - 1) / G);
     const int key_lo = a.window >= 0 ? max(0, prefix + t_first - a.window) : 0;
     const int key_hi = a.causal ? min(seq, prefix + t_last + 1) : seq;
-    const int nt = key_hi > key_lo ? (key_hi - key_lo + kAnyKeys - 1) / kAnyKeys : 0;
+    const int nt = key_hi > key_lo ? (key_hi - key_lo + kKT - 1) / kKT : 0;
     const int i_lo = shared ? 0 : split * nt / kAnyWaves;
     const int i_hi = shared ? nt : (split + 1) * nt / kAnyWaves;
 
@@ -182,9 +185,9 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // lane c holds tile i's key c: its page, then its slot
+    // lane l holds tile i's key l % kKT: its page, then its slot
     auto key_pos = [&](int i) __attribute__((always_inline)) -> int {
-      return min(key_lo + i * kAnyKeys + c, key_hi - 1);
+      return min(key_lo + i * kKT + (lane & (kKT - 1)), key_hi - 1);
     };
     auto page_load = [&](int i) __attribute__((always_inline)) -> int {
       return gptr(a.tt.table)[seq_row * a.tt.stride + (key_pos(i) >> a.tt.page_shift)];
@@ -284,16 +287,21 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
       }
       return s2[0] + s2[1];
     };
-    // Online softmax of tile i's scores (lane (c, j): keys 4j .. 4j + 3 of row c). Returns
-    // p in fp16; `moved` (the same in every lane) says whether some row's exponent base
-    // moved, and then `alpha` is the factor the row's earlier O takes (1 for the others).
-    // The base moves only when a row's max grew by more than 2^kLazyRescale in p.
-    auto softmax = [&](int i, f32x4 s, float& alpha, bool& moved) __attribute__((always_inline)) -> u32x2 {
-      const int kb0 = key_lo + i * kAnyKeys + 4 * j;
+    // Online softmax of tile i's scores, kNS blocks of 16 keys (lane (c, j): keys
+    // 16 sb + 4j .. + 3 of row c in block sb). Writes p in fp16; `moved` (the same in
+    // every lane) says whether some row's exponent base moved, and then `alpha` is the
+    // factor the row's earlier O takes (1 for the others). The base moves only when a
+    // row's max grew by more than 2^kLazyRescale in p.
+    auto softmax = [&](int i, f32x4 (&s)[kNS], u32x2 (&pk)[kNS], float& alpha, bool& moved) __attribute__((always_inline)) {
+      float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (kb0 + e < lo_r || kb0 + e >= hi_r) s[e] = -INFINITY;
-      float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      for (int sb = 0; sb < kNS; ++sb) {
+        const int kb0 = key_lo + i * kKT + sb * kAnyKeys + 4 * j;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (kb0 + e < lo_r || kb0 + e >= hi_r) s[sb][e] = -INFINITY;
+        mx = fmaxf(mx, fmaxf(fmaxf(s[sb][0], s[sb][1]), fmaxf(s[sb][2], s[sb][3])));
+      }
       alpha = 1.f;
       moved = __builtin_amdgcn_ballot_w64((mx - m_run) * a.scale_log2 > kLazyRescale) != 0;
       if (moved) {
@@ -306,17 +314,23 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
         lsum *= alpha;
       }
       const float msc = (m_run == -INFINITY ? 0.f : m_run) * a.scale_log2;
-      float p[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(s[e] * a.scale_log2 - msc);
-      lsum += (p[0] + p[1]) + (p[2] + p[3]);
-      return u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
+      for (int sb = 0; sb < kNS; ++sb) {
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(s[sb][e] * a.scale_log2 - msc);
+        lsum += (p[0] + p[1]) + (p[2] + p[3]);
+        pk[sb] = u32x2{pack_f16(p[0], p[1]), pack_f16(p[2], p[3])};
+      }
     };
     // softmax and PV of tile i in split mode (its V in this wave's LDS rows at vt)
     auto finish = [&](int i, f32x4 s, uint32_t vt) __attribute__((always_inline)) {
       float alpha;
       bool moved;
-      const u32x2 pk = softmax(i, s, alpha, moved);
+      f32x4 sa[kNS] = {s};
+      u32x2 pka[kNS];
+      softmax(i, sa, pka, alpha, moved);
+      const u32x2 pk = pka[0];
       if (moved) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) o[db] *= alpha;
@@ -348,7 +362,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
 
     // LDS words of the shared mode's exchange memory
     const uint32_t xbase = smem_base + kRing;
-    auto xp = [&](int i, int w) -> uint32_t { return xbase + kXP + ((i & 1) * kAnyWaves + w) * 512; };
+    auto xp = [&](int i, int w, int sb) -> uint32_t { return xbase + kXP + (((i & 1) * kAnyWaves + w) * kNS + sb) * 512; };
     auto xa = [&](int i, int w) -> uint32_t { return xbase + kXA + ((i & 1) * kAnyWaves + w) * (kAnyRows * 4); };
     auto xf = [&](int i) -> uint32_t { return xbase + kXF + (i & 1) * (kAnyWaves * 4); };
     if (shared && nt > 0) {
@@ -427,24 +441,34 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
         pg = pn;
         float alpha;
         bool moved;
-        const u32x2 pk = softmax(i, scores_lds(stage(i)), alpha, moved);
-        *reinterpret_cast<__attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, wave) + lane * 8)) = pk;
+        f32x4 sc[kNS];
+        u32x2 pk[kNS];
+#pragma unroll
+        for (int sb = 0; sb < kNS; ++sb) sc[sb] = scores_lds(stage(i) + sb * kAnyKeys * kRowK);
+        softmax(i, sc, pk, alpha, moved);
+#pragma unroll
+        for (int sb = 0; sb < kNS; ++sb)
+          *reinterpret_cast<__attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, wave, sb) + lane * 8)) = pk[sb];
         if (lane == 0) *reinterpret_cast<__attribute__((address_space(3))) uint32_t*>((uintptr_t)(xf(i) + wave * 4)) = moved;
         if (moved && j == 0) *reinterpret_cast<__attribute__((address_space(3))) float*>((uintptr_t)(xa(i, wave) + c * 4)) = alpha;
         // O^T[d][row] += V^T[d][key] P^T[key][row] for this wave's kCB dim blocks and the
         // four row blocks: each V^T fragment is read once (before the barrier: its stage was
         // published by the previous one) and meets four P fragments
         const uint32_t vb = stage(i) + kKTile + (4 * j + (c >> 2)) * kRowL + (c & 3) * 8 + wave * kCB * 32;
-        u32x2 vf[kCB], pf[kAnyWaves];
+        u32x2 vf[kNS][kCB], pf[kNS][kAnyWaves];
 #pragma unroll
-        for (int cb = 0; cb < kCB; ++cb)
-          vf[cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) i16x4*)(uintptr_t)(vb + cb * 32)));
+        for (int sb = 0; sb < kNS; ++sb)
+#pragma unroll
+          for (int cb = 0; cb < kCB; ++cb)
+            vf[sb][cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(uintptr_t)(vb + sb * kAnyKeys * kRowL + cb * 32)));
         __syncthreads();
         const u32x4 fl = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)xf(i));
 #pragma unroll
-        for (int rb = 0; rb < kAnyWaves; ++rb)
-          pf[rb] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, rb) + lane * 8));
+        for (int sb = 0; sb < kNS; ++sb)
+#pragma unroll
+          for (int rb = 0; rb < kAnyWaves; ++rb)
+            pf[sb][rb] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, rb, sb) + lane * 8));
         // the rows whose exponent base moved take their factor in this wave's dims
 #pragma unroll
         for (int rb = 0; rb < kAnyWaves; ++rb) {
@@ -455,11 +479,14 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
           }
         }
 #pragma unroll
-        for (int cb = 0; cb < kCB; ++cb)
+        for (int sb = 0; sb < kNS; ++sb)
 #pragma unroll
-          for (int rb = 0; rb < kAnyWaves; ++rb)
-            o[rb * kCB + cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-                __builtin_bit_cast(f16x4, vf[cb]), __builtin_bit_cast(f16x4, pf[rb]), o[rb * kCB + cb], 0, 0, 0);
+          for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+            for (int rb = 0; rb < kAnyWaves; ++rb)
+              o[rb * kCB + cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, vf[sb][cb]),
+                                                                       __builtin_bit_cast(f16x4, pf[sb][rb]),
+                                                                       o[rb * kCB + cb], 0, 0, 0);
       };
       // the odd last step runs after the loop, so the loop's back edge is its only path
       // to the next pass and the compiler's load counts stay exact there
