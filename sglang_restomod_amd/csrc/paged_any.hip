@@ -42,6 +42,11 @@ template <bool SHARED>
 struct AnyMode {
   static constexpr bool shared = SHARED;
 };
+// a register buffer index, fixed at compile time
+template <int N>
+struct AnyIdx {
+  static constexpr int v = N;
+};
 
 // SHARED: the extend kernel (work list, shared K/V ring); otherwise decode and verify
 // (split keys). Two workgroups share a CU where the registers allow it.
@@ -498,7 +503,45 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
       }
       if (i < nt) tile_step(i, kraw1, vraw1);
     }
-    if (!shared && i_hi > i_lo) {
+    if (!shared && DP <= 128 && i_hi > i_lo) {
+      // Up to 128 dims a tile is small and its compute short, so each wave keeps two tiles
+      // in flight: step i issues the slot lookup of tile i+3, writes tile i's V to LDS,
+      // loads tile i+2 into the buffers tile i-1 has left, and computes tile i. The
+      // prologue issues its loads in the steps' order. Tiles past the last are the last
+      // again (key positions clamp), so every step issues the same loads on every path.
+      u32x4 kq[3][kKL];
+      VRaw vq[3][kUL];
+      const int pa = page_load(i_lo);
+      const int pb = page_load(i_lo + 1);
+      load_v(slot_of(i_lo, pa), vq[0]);
+      load_k(slot_of(i_lo, pa), kq[0]);
+      int pc = page_load(i_lo + 2);
+      __builtin_amdgcn_sched_barrier(0);  // the lookup stays ahead of the loads after it
+      load_v(slot_of(i_lo + 1, pb), vq[1]);
+      load_k(slot_of(i_lo + 1, pb), kq[1]);
+      auto step3 = [&](int i, auto cur_t) __attribute__((always_inline)) {
+        constexpr int cur = decltype(cur_t)::v;
+        constexpr int nx = (cur + 2) % 3;
+        const int pn = page_load(i + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        write_v(vq[cur]);
+        const int sn = slot_of(i + 2, pc);
+        load_v(sn, vq[nx]);
+        load_k(sn, kq[nx]);
+        finish(i, scores(kq[cur]), lds_base);
+        pc = pn;
+      };
+      int i = i_lo;
+#pragma unroll 1
+      for (; i + 2 < i_hi; i += 3) {
+        step3(i, AnyIdx<0>{});
+        step3(i + 1, AnyIdx<1>{});
+        step3(i + 2, AnyIdx<2>{});
+      }
+      if (i < i_hi) step3(i, AnyIdx<0>{});
+      if (i + 1 < i_hi) step3(i + 1, AnyIdx<1>{});
+    }
+    if (!shared && DP > 128 && i_hi > i_lo) {
       // Step i issues the slot lookup of tile i+2, writes tile i's V to LDS and refills the
       // V registers with tile i+1, and loads tile i+1's K (into the other K buffer, or at
       // the widest head dims into the same one once tile i's scores have used it), so every
