@@ -4,18 +4,21 @@
 // sglang_restomod/attention/v100/tilelang/_kernels_paged.py:397-418; above 256 its linear
 // verify also runs on the ordinary paged kernel, _paged_adapter.py:612-616).
 //
-// One kernel serves decode, linear verify and extend rows. A wave computes 16 query rows
-// (token, GQA head) of one sequence and kv head over 16-key tiles:
+// One kernel family serves decode, linear verify and extend rows. A wave computes the
+// scores of 16 query rows (token, GQA head) of one sequence and kv head, 16 keys at a
+// time:
 //   - scores S^T = K Q^T on 16x16x32 MFMAs (the query's 16-bit type; fp8 K converted),
 //     so each lane holds four keys of one row: the B operand of the 16x16x16 fp16 MFMA
 //     of O^T += V^T P^T, whose A operand is read transposed (ds_read_b64_tr_b16) from
 //     fp16 V rows in LDS,
 //   - an online softmax with the tuned kernels' lazy rescale (kLazyRescale).
 // Decode and verify (no work list): the four waves of a workgroup hold the same 16 rows
-// and take a quarter of their key tiles each, K straight into operand registers and V
-// through the wave's own LDS rows, then merge through LDS. Extend (the work list): the
-// four waves hold 64 consecutive rows and share each K/V tile through a two-stage LDS
-// ring, one barrier per tile.
+// and take a quarter of their 16-key tiles each, K straight into operand registers and V
+// through the wave's own LDS rows, then merge through LDS. Extend (the work list, its own
+// instantiation): the four waves hold 64 consecutive rows and share each K/V tile (32
+// keys up to 128 dims, else 16) through a three-stage LDS ring; each wave publishes its
+// rows' P and accumulates O for a quarter of the dims of all 64 rows, one barrier per
+// tile.
 // The kernel is as wide as the next of 64, 128, 256 and 512: lanes past the head dim
 // read the row's last dims again (every load is unconditional), which meet Q's zeros in
 // the scores and fill output dims that are never stored.
