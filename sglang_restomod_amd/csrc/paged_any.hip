@@ -381,8 +381,12 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
       // i's P; stage (i+2) % 3, which step i+1 writes, was last read before the barrier
       // of step i-1, and so were the exchange words of tile i-2. Tiles past the last are
       // the last again (key positions clamp), every load is unconditional.
-      u32x4 kraw0[kUW], kraw1[kUW];
-      VRaw vraw0[kUW], vraw1[kUW];
+      // tile t's raw units live in register buffer t % kRB from the step that loads them
+      // (t - kRB - 1) to the step that writes them to LDS (t - 1): kRB tiles' compute to
+      // land in (three at the widest head dim, where one wave per SIMD leaves the registers)
+      constexpr int kRB = DP >= 512 ? 3 : 2;
+      u32x4 kraw[kRB][kUW];
+      VRaw vraw[kRB][kUW];
       auto load_units = [&](int myslot, u32x4 (&kraw)[kUW], VRaw (&vraw)[kUW]) __attribute__((always_inline)) {
 #pragma unroll
         for (int x = 0; x < kUW; ++x) {
@@ -427,26 +431,31 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
         }
       };
       auto stage = [&](int i) -> uint32_t { return smem_base + (uint32_t)(i % 3) * kStageB; };
-      // tile t's raw units live in buffer t % 2 from the step that loads them (t - 3) to
-      // the step that writes them to LDS (t - 1): two tiles' compute to land in
-      // (the prologue issues its loads in the steps' order, each page lookup ahead of the
-      // units before it, so the loop starts with the load counts its back edge brings)
-      const int pg0 = page_load(0);
-      const int pg1 = page_load(1);
-      load_units(slot_of(0, pg0), kraw0, vraw0);
-      const int pg2 = page_load(2);
-      load_units(slot_of(1, pg1), kraw1, vraw1);
-      write_units(stage(0), kraw0, vraw0);
-      int pg = page_load(3);
-      load_units(slot_of(2, pg2), kraw0, vraw0);
+      // Page lookups go out two steps before the units that use them: waiting for a lookup
+      // then waits only for loads issued before it, which have had kRB steps to land. The
+      // prologue issues its loads in the steps' order, so the loop starts with the load
+      // counts its back edge brings.
+      int pa = page_load(0);
+      int pb = page_load(1);
+      int pc = page_load(2);
+#pragma unroll
+      for (int t = 0; t < kRB; ++t) {
+        load_units(slot_of(t, pa), kraw[t], vraw[t]);
+        pa = pb;
+        pb = pc;
+        pc = page_load(t + 3);
+      }
+      write_units(stage(0), kraw[0], vraw[0]);
+      load_units(slot_of(kRB, pa), kraw[0], vraw[0]);
+      int pg1 = pb, pg2 = pc;  // the pages of tiles kRB + 1 and kRB + 2
       __syncthreads();
-      auto tile_step = [&](int i, u32x4 (&kn)[kUW], VRaw (&vn)[kUW]) __attribute__((always_inline)) {
-        write_units(stage(i + 1), kn, vn);       // tile i+1, buffer (i+1) % 2
-        // the next page lookup goes out before the unit loads, so the step that uses it
-        // waits for it alone, not for the units behind it
-        const int pn = page_load(i + 4);
-        load_units(slot_of(i + 3, pg), kn, vn);  // tile i+3 into the buffer just written
-        pg = pn;
+      auto tile_step = [&](int i, auto buf_t) __attribute__((always_inline)) {
+        constexpr int cur = decltype(buf_t)::v;  // (i + 1) % kRB
+        write_units(stage(i + 1), kraw[cur], vraw[cur]);  // tile i+1
+        const int pn = page_load(i + kRB + 3);
+        load_units(slot_of(i + kRB + 1, pg1), kraw[cur], vraw[cur]);  // into the buffer just written
+        pg1 = pg2;
+        pg2 = pn;
         float alpha;
         bool moved;
         f32x4 sc[kNS];
@@ -496,15 +505,20 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
                                                                        __builtin_bit_cast(f16x4, pf[sb][rb]),
                                                                        o[rb * kCB + cb], 0, 0, 0);
       };
-      // the odd last step runs after the loop, so the loop's back edge is its only path
-      // to the next pass and the compiler's load counts stay exact there
+      // the last steps short of a whole round of buffers run after the loop, so the loop's
+      // back edge is its only path to the next pass and the compiler's load counts stay
+      // exact there
       int i = 0;
 #pragma unroll 1
-      for (; i + 1 < nt; i += 2) {
-        tile_step(i, kraw1, vraw1);
-        tile_step(i + 1, kraw0, vraw0);
+      for (; i + kRB - 1 < nt; i += kRB) {
+        tile_step(i, AnyIdx<1 % kRB>{});
+        tile_step(i + 1, AnyIdx<2 % kRB>{});
+        if constexpr (kRB == 3) tile_step(i + 2, AnyIdx<0>{});
       }
-      if (i < nt) tile_step(i, kraw1, vraw1);
+      if (i < nt) tile_step(i, AnyIdx<1 % kRB>{});
+      if constexpr (kRB == 3) {
+        if (i + 1 < nt) tile_step(i + 1, AnyIdx<2 % kRB>{});
+      }
     }
     if (!shared && DP <= 128 && i_hi > i_lo) {
       // Up to 128 dims a tile is small and its compute short, so each wave keeps two tiles
