@@ -83,8 +83,9 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
   constexpr int kQBlock = kQLds ? kAnyRows * kQRow : 0;  // one wave's Q rows
   // Extend rows: the four waves own 64 consecutive rows of one sequence and kv head and
   // share every K/V tile (kKT keys: 32 up to 128 dims, else 16) through a three-stage LDS
-  // ring (16-bit K rows padded by 16 bytes, fp16 V rows as above), loaded once per
-  // workgroup; kUW 16-byte units per thread. Each wave computes the scores and softmax of
+  // ring (16-bit K rows padded by 16 bytes, V rows padded as above: fp16, or bf16 that
+  // becomes fp16 as its fragments are read), loaded once per workgroup; kUW 16-byte
+  // units per thread. Each wave computes the scores and softmax of
   // its own 16 rows, and O for a quarter of the dims (kCB 16-dim blocks) of all 64 rows:
   // P, the rescale factors and their flags pass through the exchange memory behind the
   // ring (two tiles deep). Decode and verify tiles have 16 keys.
@@ -416,14 +417,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
               vh = cvt8_fp8<KV, false>(vraw[x][0], vraw[x][1]);
             } else {
               kh = kraw[x];
-              if constexpr (QBF16) {
-#pragma unroll
-                for (int w = 0; w < 4; ++w)
-                  vh[w] = pack_f16(__builtin_bit_cast(float, vraw[x][w] << 16),
-                                   __builtin_bit_cast(float, vraw[x][w] & 0xffff0000u));
-              } else {
-                vh = vraw[x];
-              }
+              vh = vraw[x];  // bf16 V stays bf16 in LDS: its fragments are converted as read
             }
             *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(st + key * kRowK + q * 16)) = kh;
             *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(st + kKTile + key * kRowL + q * 16)) = vh;
@@ -480,6 +474,18 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
             vf[sb][cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) i16x4*)(uintptr_t)(vb + sb * kAnyKeys * kRowL + cb * 32)));
         __syncthreads();
+        if constexpr (QBF16 && !kFp8) {
+          // bf16 V fragments to fp16 (each V element is read by one wave only, so this is
+          // the same conversion count as converting the tile when it is written)
+#pragma unroll
+          for (int sb = 0; sb < kNS; ++sb)
+#pragma unroll
+            for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+              for (int w = 0; w < 2; ++w)
+                vf[sb][cb][w] = pack_f16(__builtin_bit_cast(float, vf[sb][cb][w] << 16),
+                                         __builtin_bit_cast(float, vf[sb][cb][w] & 0xffff0000u));
+        }
         const u32x4 fl = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)xf(i));
 #pragma unroll
         for (int sb = 0; sb < kNS; ++sb)
