@@ -45,11 +45,13 @@ def common_flags() -> list[str]:
     ]
 
 
-# Flags of single sources. paged_any's kernels hold their MFMA accumulators in ordinary
-# VGPRs: with them in AGPRs, the online-softmax rescale (VALU, which cannot address AGPRs)
-# made the register allocator copy the whole output block between the two register files
-# on every key tile.
-SOURCE_FLAGS = {"paged_any": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Flags of single sources. The decode/verify kernels (splitkv, paged_any) hold their MFMA
+# accumulators in ordinary VGPRs: with them in AGPRs, the online-softmax rescale (VALU,
+# which cannot address AGPRs) made the register allocator copy the whole output block
+# between the two register files on every key tile (hundreds to thousands of
+# v_accvgpr moves per kernel).
+_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+SOURCE_FLAGS = {"paged_any": _VGPR_FORM, "splitkv": _VGPR_FORM}
 
 
 def _flags(src: Path, extra: list[str]) -> list[str]:
