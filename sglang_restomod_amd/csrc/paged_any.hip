@@ -375,13 +375,14 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
     auto xa = [&](int i, int w) -> uint32_t { return xbase + kXA + ((i & 1) * kAnyWaves + w) * (kAnyRows * 4); };
     auto xf = [&](int i) -> uint32_t { return xbase + kXF + (i & 1) * (kAnyWaves * 4); };
     if (shared && nt > 0) {
-      // The workgroup's tile ring. Step i writes tile i+1 (loaded during step i-1) to stage
-      // (i+1) % 3, loads tile i+3, computes the scores and softmax of tile i from stage
-      // i % 3 and publishes P, then meets the other waves, then accumulates PV for its
-      // dims from every wave's P. The barrier of step i publishes stage (i+1) % 3 and tile
-      // i's P; stage (i+2) % 3, which step i+1 writes, was last read before the barrier
-      // of step i-1, and so were the exchange words of tile i-2. Tiles past the last are
-      // the last again (key positions clamp), every load is unconditional.
+      // The workgroup's tile ring. Step i writes tile i+1 (its units loaded kRB steps
+      // earlier) to stage (i+1) % 3, loads tile i+kRB+1, computes the scores and softmax
+      // of tile i from stage i % 3 and publishes P, then meets the other waves, then
+      // accumulates PV for its dims from every wave's P. The barrier of step i publishes
+      // stage (i+1) % 3 and tile i's P; stage (i+2) % 3, which step i+1 writes, was last
+      // read before the barrier of step i-1, and so were the exchange words of tile i-2.
+      // Tiles past the last are the last again (key positions clamp), every load is
+      // unconditional.
       // tile t's raw units live in register buffer t % kRB from the step that loads them
       // (t - kRB - 1) to the step that writes them to LDS (t - 1): kRB tiles' compute to
       // land in (three at the widest head dim, where one wave per SIMD leaves the registers)
