@@ -1,5 +1,6 @@
 """Seeded generators for the benchmark workloads: five at head dim 128 (0-4), two at
-head dim 256 (5, 6) and two at head dim 512 (7, 8).
+head dim 256 (5, 6) and two at head dim 512 (7, 8); 9 and 10 are the extend batch of 8 at
+head dims 96 and 192 (parity cases of the any-head-dim kernel's extend).
 
 Seeding scheme: one CPU ``torch.Generator`` per workload with seed = workload
 index. Draw order: lengths, slot permutation, then (on the target device,
@@ -42,6 +43,10 @@ WORKLOADS = {
             heads=16, heads_kv=4, dim=512, dtype="bf16", kv="bf16"),
     8: dict(name="extend_b8_p0-4k_e256-2k_h16kv4_d512_bf16", mode="extend", batch=8,
             prefix=(0, 4096), extend=(256, 2048), heads=16, heads_kv=4, dim=512, dtype="bf16", kv="bf16"),
+    9: dict(name="extend_b8_p0-4k_e256-2k_h32kv8_d96_bf16", mode="extend", batch=8,
+            prefix=(0, 4096), extend=(256, 2048), heads=32, heads_kv=8, dim=96, dtype="bf16", kv="bf16"),
+    10: dict(name="extend_b8_p0-4k_e256-2k_h16kv4_d192_fp16", mode="extend", batch=8,
+             prefix=(0, 4096), extend=(256, 2048), heads=16, heads_kv=4, dim=192, dtype="fp16", kv="fp16"),
 }
 
 _DT = {"fp16": torch.float16, "bf16": torch.bfloat16}

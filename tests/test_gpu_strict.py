@@ -7,8 +7,8 @@
   (an exact result rounded to bf16 is already up to half an ulp away).
 
 Workloads: decode B=1 (fp16), decode B=64 (bf16), fp8 decode B=128 in e4m3 and e5m2,
-verify B=32 x 4, extend B=8 (every row), and the head-dim-256 and head-dim-512 decode
-and extend.
+verify B=32 x 4, extend B=8 (every row), the head-dim-256 and head-dim-512 decode and
+extend, and the extend batch at head dims 96 (bf16) and 192 (fp16).
 """
 
 from __future__ import annotations
@@ -55,7 +55,7 @@ def _half_ulp(ref: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 
 CASES = [(0, "e4m3"), (1, "e4m3"), (3, "e4m3"), (3, "e5m2"), (4, "e4m3"), (2, "e4m3"), (5, "e4m3"), (6, "e4m3"),
-         (7, "e4m3"), (8, "e4m3")]
+         (7, "e4m3"), (8, "e4m3"), (9, "e4m3"), (10, "e4m3")]
 
 
 @pytest.mark.parametrize("index,fmt", CASES)
