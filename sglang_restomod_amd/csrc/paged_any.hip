@@ -444,29 +444,11 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
       load_units(slot_of(kRB, pa), kraw[0], vraw[0]);
       int pg1 = pb, pg2 = pc;  // the pages of tiles kRB + 1 and kRB + 2
       __syncthreads();
-      auto tile_step = [&](int i, auto buf_t) __attribute__((always_inline)) {
-        constexpr int cur = decltype(buf_t)::v;  // (i + 1) % kRB
-        write_units(stage(i + 1), kraw[cur], vraw[cur]);  // tile i+1
-        const int pn = page_load(i + kRB + 3);
-        load_units(slot_of(i + kRB + 1, pg1), kraw[cur], vraw[cur]);  // into the buffer just written
-        pg1 = pg2;
-        pg2 = pn;
-        float alpha;
-        bool moved;
-        f32x4 sc[kNS];
-        u32x2 pk[kNS];
-#pragma unroll
-        for (int sb = 0; sb < kNS; ++sb) sc[sb] = scores_lds(stage(i) + sb * kAnyKeys * kRowK);
-        softmax(i, sc, pk, alpha, moved);
-#pragma unroll
-        for (int sb = 0; sb < kNS; ++sb)
-          *reinterpret_cast<__attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, wave, sb) + lane * 8)) = pk[sb];
-        if (lane == 0) *reinterpret_cast<__attribute__((address_space(3))) uint32_t*>((uintptr_t)(xf(i) + wave * 4)) = moved;
-        if (moved && j == 0) *reinterpret_cast<__attribute__((address_space(3))) float*>((uintptr_t)(xa(i, wave) + c * 4)) = alpha;
-        // O^T[d][row] += V^T[d][key] P^T[key][row] for this wave's kCB dim blocks and the
-        // four row blocks: each V^T fragment is read once (before the barrier: its stage was
-        // published by the previous one) and meets four P fragments
-        const uint32_t vb = stage(i) + kKTile + (4 * j + (c >> 2)) * kRowL + (c & 3) * 8 + wave * kCB * 32;
+      // PV of tile t: the V^T fragments of this wave's kCB dim blocks (stage t % 3) meet
+      // the P fragments of all four row blocks, after the rows whose exponent base moved
+      // have taken their factor
+      auto pv = [&](int t) __attribute__((always_inline)) {
+        const uint32_t vb = stage(t) + kKTile + (4 * j + (c >> 2)) * kRowL + (c & 3) * 8 + wave * kCB * 32;
         u32x2 vf[kNS][kCB], pf[kNS][kAnyWaves];
 #pragma unroll
         for (int sb = 0; sb < kNS; ++sb)
@@ -474,7 +456,12 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
           for (int cb = 0; cb < kCB; ++cb)
             vf[sb][cb] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) i16x4*)(uintptr_t)(vb + sb * kAnyKeys * kRowL + cb * 32)));
-        __syncthreads();
+        const u32x4 fl = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)xf(t));
+#pragma unroll
+        for (int sb = 0; sb < kNS; ++sb)
+#pragma unroll
+          for (int rb = 0; rb < kAnyWaves; ++rb)
+            pf[sb][rb] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(t, rb, sb) + lane * 8));
         if constexpr (QBF16 && !kFp8) {
           // bf16 V fragments to fp16 (each V element is read by one wave only, so this is
           // the same conversion count as converting the tile when it is written)
@@ -487,17 +474,10 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
                 vf[sb][cb][w] = pack_f16(__builtin_bit_cast(float, vf[sb][cb][w] << 16),
                                          __builtin_bit_cast(float, vf[sb][cb][w] & 0xffff0000u));
         }
-        const u32x4 fl = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)xf(i));
-#pragma unroll
-        for (int sb = 0; sb < kNS; ++sb)
-#pragma unroll
-          for (int rb = 0; rb < kAnyWaves; ++rb)
-            pf[sb][rb] = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, rb, sb) + lane * 8));
-        // the rows whose exponent base moved take their factor in this wave's dims
 #pragma unroll
         for (int rb = 0; rb < kAnyWaves; ++rb) {
           if (__builtin_amdgcn_readfirstlane(fl[rb])) {
-            const float al = *reinterpret_cast<const __attribute__((address_space(3))) float*>((uintptr_t)(xa(i, rb) + c * 4));
+            const float al = *reinterpret_cast<const __attribute__((address_space(3))) float*>((uintptr_t)(xa(t, rb) + c * 4));
 #pragma unroll
             for (int cb = 0; cb < kCB; ++cb) o[rb * kCB + cb] *= al;
           }
@@ -511,6 +491,30 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
               o[rb * kCB + cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, vf[sb][cb]),
                                                                        __builtin_bit_cast(f16x4, pf[sb][rb]),
                                                                        o[rb * kCB + cb], 0, 0, 0);
+      };
+      // Step i: the scores of tile i, then PV of tile i-1 (independent work for the MFMA
+      // pipe while the scores land), then tile i's softmax, whose P the barrier publishes.
+      auto tile_step = [&](int i, auto buf_t) __attribute__((always_inline)) {
+        constexpr int cur = decltype(buf_t)::v;  // (i + 1) % kRB
+        write_units(stage(i + 1), kraw[cur], vraw[cur]);  // tile i+1
+        const int pn = page_load(i + kRB + 3);
+        load_units(slot_of(i + kRB + 1, pg1), kraw[cur], vraw[cur]);  // into the buffer just written
+        pg1 = pg2;
+        pg2 = pn;
+        float alpha;
+        bool moved;
+        f32x4 sc[kNS];
+        u32x2 pk[kNS];
+#pragma unroll
+        for (int sb = 0; sb < kNS; ++sb) sc[sb] = scores_lds(stage(i) + sb * kAnyKeys * kRowK);
+        if (i > 0) pv(i - 1);
+        softmax(i, sc, pk, alpha, moved);
+#pragma unroll
+        for (int sb = 0; sb < kNS; ++sb)
+          *reinterpret_cast<__attribute__((address_space(3))) u32x2*>((uintptr_t)(xp(i, wave, sb) + lane * 8)) = pk[sb];
+        if (lane == 0) *reinterpret_cast<__attribute__((address_space(3))) uint32_t*>((uintptr_t)(xf(i) + wave * 4)) = moved;
+        if (moved && j == 0) *reinterpret_cast<__attribute__((address_space(3))) float*>((uintptr_t)(xa(i, wave) + c * 4)) = alpha;
+        __syncthreads();
       };
       // the last steps short of a whole round of buffers run after the loop, so the loop's
       // back edge is its only path to the next pass and the compiler's load counts stay
@@ -526,6 +530,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
       if constexpr (kRB == 3) {
         if (i + 1 < nt) tile_step(i + 1, AnyIdx<2 % kRB>{});
       }
+      pv(nt - 1);
     }
     if (!shared && DP <= 128 && i_hi > i_lo) {
       // Up to 128 dims a tile is small and its compute short, so each wave keeps two tiles
