@@ -74,9 +74,9 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
   static_assert(!kFp8 || KK % 2 == 0, "fp8 K loads cover two QK steps");
   typedef typename AnyVRaw<kFp8>::type VRaw;
 
-  // At the widest head dim with 16-bit KV, Q lives in LDS (rows padded by 16 bytes so the
-  // 16 rows of an operand read fall in different banks): its 64 registers are what the
-  // prefetched K and V need.
+  // Decode and verify at the widest head dim with 16-bit KV keep Q in LDS (rows padded by
+  // 16 bytes so the 16 rows of an operand read fall in different banks): its 64 registers
+  // are what the prefetched K and V need. Extend keeps Q in registers.
   constexpr bool kQLds = DP >= 512 && !kFp8;
   constexpr int kQRow = DP * 2 + 16;
   constexpr int kVBlock = kAnyKeys * kRowL;            // one wave's V rows
@@ -85,10 +85,10 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
   // share every K/V tile (kKT keys: 32 up to 128 dims, else 16) through a three-stage LDS
   // ring (16-bit K rows padded by 16 bytes, V rows padded as above: fp16, or bf16 that
   // becomes fp16 as its fragments are read), loaded once per workgroup; kUW 16-byte
-  // units per thread. Each wave computes the scores and softmax of
-  // its own 16 rows, and O for a quarter of the dims (kCB 16-dim blocks) of all 64 rows:
-  // P, the rescale factors and their flags pass through the exchange memory behind the
-  // ring (two tiles deep). Decode and verify tiles have 16 keys.
+  // units per thread. Each wave computes the scores and softmax of its own 16 rows, and
+  // O for a quarter of the dims (kCB 16-dim blocks) of all 64 rows: P, the rescale
+  // factors and their flags pass through the exchange memory behind the ring (two tiles
+  // deep). Decode and verify tiles have 16 keys.
   constexpr int kKT = (SHARED && DP <= 128) ? 2 * kAnyKeys : kAnyKeys;
   constexpr int kNS = kKT / kAnyKeys;  // 16-key score blocks per tile
   constexpr int kRowK = DP * 2 + 16;
