@@ -74,10 +74,11 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
   static_assert(!kFp8 || KK % 2 == 0, "fp8 K loads cover two QK steps");
   typedef typename AnyVRaw<kFp8>::type VRaw;
 
-  // Decode and verify at the widest head dim with 16-bit KV keep Q in LDS (rows padded by
-  // 16 bytes so the 16 rows of an operand read fall in different banks): its 64 registers
-  // are what the prefetched K and V need. Extend keeps Q in registers.
-  constexpr bool kQLds = DP >= 512 && !kFp8;
+  // Decode and verify at the widest head dim with fp16 Q and KV keep Q in LDS (rows padded
+  // by 16 bytes so the 16 rows of an operand read fall in different banks): in registers
+  // it spilled. bf16 and fp8 KV, and extend, keep Q in registers (1-3% faster at D=320
+  // and 512 than reading it from LDS every tile).
+  constexpr bool kQLds = DP >= 512 && !kFp8 && !QBF16;
   constexpr int kQRow = DP * 2 + 16;
   constexpr int kVBlock = kAnyKeys * kRowL;            // one wave's V rows
   constexpr int kQBlock = kQLds ? kAnyRows * kQRow : 0;  // one wave's Q rows
