@@ -168,6 +168,13 @@ def test_extend_reference_gpu_test_shape(gpu, prefix, extend):
     _run_synthetic(gpu, [prefix], [extend], 4, 2, dtype=torch.float16, page_size=16, dim=256)
 
 
+@pytest.mark.parametrize("dim,dtype", [(96, torch.bfloat16), (512, torch.float16)])
+def test_extend_page_size_16_table_other_head_dims(gpu, dim, dtype):
+    """The 16-token page layout through the any-head-dim kernel's extend (scattered pages,
+    prefixes that end inside a page)."""
+    _run_synthetic(gpu, [37, 0, 130], [45, 70, 19], 16, 4, dtype=dtype, page_size=16, dim=dim)
+
+
 def test_extend_ragged_batch_with_empty_sequences(gpu):
     # sequences without new tokens list no row tile; the others must still be served
     _run_synthetic(gpu, [30, 0, 400, 9, 0], [0, 70, 0, 300, 1], 40, 8)

@@ -156,6 +156,18 @@ def test_decode_page_size_16_table(gpu):
     _check_table_decode(q, k, v, table, seq, 16, out, 0.1)
 
 
+@pytest.mark.parametrize("dim,dtype", [(96, torch.bfloat16), (512, torch.float16)])
+def test_decode_page_size_16_table_other_head_dims(gpu, dim, dtype):
+    """The 16-token page layout through the any-head-dim kernel's decode."""
+    lengths = [1, 37, 53, 200]
+    q, k, v, table, seq = _synthetic(gpu, lengths, 16, 4, dim=dim, dtype=dtype, page_size=16)
+    k4 = k.view(-1, 16, 4, dim)
+    v4 = v.view(-1, 16, 4, dim)
+    out = _ops().grouped_decode_forward(q, k4, v4, table, seq, softmax_scale=dim ** -0.5)
+    torch.cuda.synchronize()
+    _check_table_decode(q, k, v, table, seq, 16, out, dim ** -0.5)
+
+
 def test_decode_zero_length_gives_zero(gpu):
     q, k, v, table, seq = _synthetic(gpu, [0, 5], 32, 8)
     out = _ops().grouped_decode_forward(q, k, v, table, seq, softmax_scale=0.1)
