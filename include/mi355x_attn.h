@@ -30,8 +30,9 @@
  * every KV dtype (the reference's paged kernels take any head dim: configurations for
  * 64, 128, 256 and 512 and a default for the rest, _kernels_paged.py:397-418). 64, 128
  * and 256 run on the split-KV and tiled extend kernels; the others on one kernel that
- * serves decode, verify and extend rows alike (16 rows per wave, no split over keys, no
- * workspace). Other head dims return MA_EUNSUPPORTED.
+ * serves decode, verify and extend rows alike (16 rows per wave; a decode also splits each
+ * sequence's keys over several workgroups when the batch alone would leave compute units
+ * idle). Other head dims return MA_EUNSUPPORTED.
  */
 #ifndef MI355X_ATTN_H
 #define MI355X_ATTN_H
@@ -43,7 +44,7 @@
 extern "C" {
 #endif
 
-#define MA_ABI_VERSION 9
+#define MA_ABI_VERSION 10
 
 /* dtype codes */
 #define MA_DT_F16 0
@@ -77,8 +78,10 @@ int ma_device_workgroups(void);
  * Bytes of workspace the split-KV entry points need for a persistent grid of
  * `num_workgroups` workgroups (1..16384): one descriptor per wave, then the partial
  * results of segments shared by several waves. No initialisation is needed; calls
- * that overlap in time must use different workspaces. 0 at the head dims other than
- * 64, 128 and 256, whose kernel needs none.
+ * that overlap in time must use different workspaces. At the head dims other than 64,
+ * 128 and 256 it holds only the key pieces of a split decode (2 * num_workgroups
+ * pieces of 16 rows); there a decode given no workspace runs without the split, and
+ * verify uses none.
  */
 size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim);
 
@@ -92,6 +95,12 @@ size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim);
  *   k/v pools as above; kv_dtype = q_dtype, MA_DT_E4M3 or MA_DT_E5M2
  *   seq_lens [batch] int32: keys of each sequence (0 gives a zero output)
  *   sliding_window: -1 for none, else keys >= seq_len - 1 - window only
+ *   max_seq_len: an upper bound of seq_lens the caller knows without reading the device
+ *     (the engine's host copy of the lengths), or 0 for none. It only chooses the kernels:
+ *     a batch whose split-KV work is small (a few thousand 32-key tiles at this bound)
+ *     runs as one pass of the any-head-dim kernel over key pieces plus a merge, which
+ *     has a shorter critical path; the result does not depend on it (each piece is a
+ *     share of its sequence's own keys), so a wrong bound costs time, never correctness.
  *   num_workgroups: persistent grid size (ma_device_workgroups() fills the chip); the
  *     key axis of every (sequence, kv head) is cut into 32-token tiles and each wave
  *     takes an equal contiguous share of all tiles (stream-K, at least 2 tiles per
@@ -108,7 +117,7 @@ int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
                       int64_t table_stride, const int64_t* row_index, int page_size,
                       const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
                       int head_dim, int num_workgroups, float softmax_scale, float k_scale,
-                      float v_scale, int sliding_window, void* workspace,
+                      float v_scale, int sliding_window, int max_seq_len, void* workspace,
                       size_t workspace_bytes, void* out, int out_dtype, int64_t out_stride_tok,
                       int64_t out_stride_head, void* stream);
 
@@ -119,8 +128,8 @@ int ma_grouped_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head
  * Same arguments and results as ma_grouped_decode minus the workspace: the split-KV
  * partials go to a static scratch array in the library's device code (one copy per GPU,
  * held from the library's first use on that GPU until the process ends) sized for
- * num_workgroups <= MA_NOALLOC_MAX_WORKGROUPS at head_dim <= 256: 67,403,776 bytes (the
- * head dims other than 64, 128 and 256 run on a kernel that uses no scratch).
+ * num_workgroups <= MA_NOALLOC_MAX_WORKGROUPS at head_dim <= 256: 67,403,776 bytes, which
+ * also holds the key pieces of a split decode at every head dim up to 512.
  * Larger grids return MA_EINVAL. Nothing is allocated or freed; the scratch needs no
  * clearing (every call rewrites what it reads). Calls that overlap in time on one GPU
  * (two streams) share the scratch and race: serialise them.
@@ -132,8 +141,9 @@ int ma_grouped_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_str
                               int64_t table_stride, const int64_t* row_index, int page_size,
                               const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads,
                               int head_dim, int num_workgroups, float softmax_scale, float k_scale,
-                              float v_scale, int sliding_window, void* out, int out_dtype,
-                              int64_t out_stride_tok, int64_t out_stride_head, void* stream);
+                              float v_scale, int sliding_window, int max_seq_len, void* out,
+                              int out_dtype, int64_t out_stride_tok, int64_t out_stride_head,
+                              void* stream);
 
 /*
  * Grouped split-KV verify: a few query tokens per sequence (linear speculative

@@ -40,7 +40,7 @@ SIGNATURES = {
         c_void_p, c_int64, c_void_p, c_int,           # table, stride, row_index, page size
         c_void_p, c_int, c_int, c_int, c_int,         # seq_lens, batch, hq, hkv, dim
         c_int, c_float, c_float, c_float,             # num_workgroups, scales
-        c_int, c_void_p, c_size_t,                    # window, workspace, bytes
+        c_int, c_int, c_void_p, c_size_t,             # window, max_seq_len, workspace, bytes
         c_void_p, c_int, c_int64, c_int64, c_void_p,  # out, out dtype, strides, stream
     ]),
     "ma_grouped_decode_noalloc": (c_int, [
@@ -49,6 +49,7 @@ SIGNATURES = {
         c_void_p, c_int64, c_void_p, c_int,           # table, stride, row_index, page size
         c_void_p, c_int, c_int, c_int, c_int,         # seq_lens, batch, hq, hkv, dim
         c_int, c_float, c_float, c_float, c_int,      # num_workgroups, scales, window
+        c_int,                                        # max_seq_len
         c_void_p, c_int, c_int64, c_int64, c_void_p,  # out, out dtype, strides, stream
     ]),
     "ma_paged_verify": (c_int, [

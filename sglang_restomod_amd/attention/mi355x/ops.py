@@ -32,6 +32,26 @@ MAX_HEAD_DIM = 512                 # other multiples of 16 up to this: the any-h
 HEAD_DIM_MULTIPLE = 16
 
 
+# A decode with at most this many 32-key split-KV tiles (over every sequence, kv head and
+# 32-row group, at the caller's length bound) runs as key pieces on the any-head-dim kernel
+# (MA_SMALL_DECODE_TILES in csrc/splitkv.hip).
+SMALL_DECODE_TILES = 16384
+
+
+def decode_kernel(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                  max_seq_len_hint: Optional[int]) -> str:
+    """Which kernel carries a decode call: ``"splitkv_partial"`` (the persistent split-KV
+    kernel) or ``"any_kernel"`` (head dims other than 64/128/256, and small decodes given a
+    length bound). The library makes the same choice."""
+    if int(head_dim) not in TUNED_HEAD_DIMS:
+        return "any_kernel"
+    if not max_seq_len_hint or max_seq_len_hint <= 0:
+        return "splitkv_partial"
+    group = int(num_q_heads) // int(num_kv_heads)
+    tiles = int(batch) * int(num_kv_heads) * ((group + 31) // 32) * ((int(max_seq_len_hint) + 31) // 32)
+    return "any_kernel" if tiles <= SMALL_DECODE_TILES else "splitkv_partial"
+
+
 def head_dim_supported(head_dim: int) -> bool:
     """Head dims the library serves: every multiple of 16 from 16 to 512 (64, 128 and 256 on
     the tuned kernels, the rest on the any-head-dim kernel, which needs no workspace)."""
@@ -252,7 +272,9 @@ def grouped_decode_forward(
     out_code = _out_code(out, q)
     seq = _i32(seq_lens)
     ridx = None if row_index is None else row_index.to(torch.int64).contiguous()
-    del max_seq_len_hint  # the persistent grid does not depend on lengths
+    # a host-known bound of the lengths picks the single-pass path for small batches; it
+    # never changes the result
+    max_len = 0 if max_seq_len_hint is None else max(0, int(max_seq_len_hint))
     nwg = int(num_workgroups) if num_workgroups else splitkv_workgroups(dev)
     lib = _lib.load()
     ws, nbytes = _splitkv_ws(lib, dev, nwg, D, workspace)
@@ -262,7 +284,7 @@ def grouped_decode_forward(
         table.data_ptr(), table.stride(0), _ptr(ridx), ps,
         seq.data_ptr(), B, Hq, Hkv, D,
         nwg, float(softmax_scale), float(k_scale), float(v_scale),
-        int(sliding_window_size), _ptr(ws), nbytes,
+        int(sliding_window_size), max_len, _ptr(ws), nbytes,
         out.data_ptr(), out_code, out.stride(0), out.stride(1), _stream_ptr(dev),
     )
     _lib.check(status, "ma_grouped_decode")

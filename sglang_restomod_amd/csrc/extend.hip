@@ -746,7 +746,7 @@ extern "C" int ma_paged_extend(
     g.tt.table = table; g.tt.stride = table_stride; g.tt.page_shift = __builtin_ctz(page_size);
     g.row_index = row_index; g.seq_lens = seq_lens; g.qsl = query_start_loc; g.prefix = prefix_lens;
     g.num_tokens = (int)num_tokens; g.batch = batch; g.hq = num_q_heads; g.hkv = num_kv_heads; g.group = group;
-    g.head_dim = head_dim; g.items = p.items; g.row_blocks = 0;
+    g.head_dim = head_dim; g.items = p.items; g.row_blocks = 0; g.pieces = 1;
     g.causal = p.causal; g.window = p.window;
     g.scale_log2 = softmax_scale * k_scale * kLog2e; g.v_scale = v_scale;
     g.out = out; g.out_stride_tok = out_stride_tok; g.out_stride_head = out_stride_head;

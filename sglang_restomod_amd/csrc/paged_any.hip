@@ -113,6 +113,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
   static_assert(kBPR >= 1 && kBPR * kAnyWaves * 1024 <= kSmem, "merge rounds fit the kernel's LDS");
   __shared__ __attribute__((aligned(256))) unsigned char smem[kSmem];
   __shared__ float mrow[kAnyWaves][2][kAnyRows];  // each wave's row max and row sum of p
+  int64_t piece_slot = 0;  // decode with pieces > 1: where this workgroup's partial goes
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -186,8 +187,10 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
     const int key_lo = a.window >= 0 ? max(0, prefix + t_first - a.window) : 0;
     const int key_hi = a.causal ? min(seq, prefix + t_last + 1) : seq;
     const int nt = key_hi > key_lo ? (key_hi - key_lo + kKT - 1) / kKT : 0;
-    const int i_lo = shared ? 0 : split * nt / kAnyWaves;
-    const int i_hi = shared ? nt : (split + 1) * nt / kAnyWaves;
+    // split: this wave's quarter of the workgroup's key piece (pieces x 4 equal shares)
+    const int parts = kAnyWaves * a.pieces;
+    const int i_lo = shared ? 0 : (int)((int64_t)split * nt / parts);
+    const int i_hi = shared ? nt : (int)((int64_t)(split + 1) * nt / parts);
 
     float m_run = -INFINITY;
     float lsum = 0.f;  // this lane's share of its row's sum of p (keys 4j .. 4j + 3 of each tile)
@@ -666,6 +669,18 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
       ltot += mrow[u][1][c] * sc[u];
     }
     const float inv = (ltot > 0.f) ? a.v_scale / ltot : 0.f;
+    // one piece of several (pieces > 1): this workgroup's rows normalised over its keys,
+    // in fp32, and their log2 LSE, for the merge kernel; every row is written (a row that
+    // saw no key gets O = 0 and LSE -inf)
+    const bool piece_out = a.pieces > 1;
+    float MA_GLOBAL* po = nullptr;
+    if (piece_out) {
+      po = gptr_mut(a.part_o) + (int64_t)piece_slot * (16 * DP) + c * DP + 4 * j;
+      if (wave == 0 && j == 0)
+        gptr_mut(a.part_lse)[(int64_t)piece_slot * 16 + c] =
+            (ltot > 0.f) ? __builtin_amdgcn_logf(ltot) + mmax * a.scale_log2 : -INFINITY;
+    }
+    const float pinv = (ltot > 0.f) ? 1.f / ltot : 0.f;
 #pragma unroll
     for (int r = 0; r < DB; r += kBPR) {
 #pragma unroll
@@ -680,7 +695,10 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
         for (int u = 0; u < kAnyWaves; ++u)
           acc += *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(
                      (uintptr_t)(smem_base + ((u * kBPR + blk) * 64 + lane) * 16)) * sc[u];
-        if (real && (r + blk) * 16 < D) store_out4<QBF16>(a.out, off + (r + blk) * 16 + 4 * j, acc, inv, a.out_f32);
+        if (piece_out)
+          *reinterpret_cast<f32x4 MA_GLOBAL*>(po + (r + blk) * 16) = acc * pinv;
+        else if (real && (r + blk) * 16 < D)
+          store_out4<QBF16>(a.out, off + (r + blk) * 16 + 4 * j, acc, inv, a.out_f32);
       }
       __syncthreads();  // before the next round (or the next row block) reuses the memory
     }
@@ -698,20 +716,118 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
     for (int pass = 0; pass < kAnyPlanRows / (kAnyWaves * kAnyRows); ++pass)
       rows(AnyMode<true>{}, b, h, rt * kAnyPlanRows + pass * (kAnyWaves * kAnyRows) + wave * kAnyRows, -1);
   } else {
-    // decode and verify: workgroup item = (kv head, 16-row block, sequence), kv head
-    // fastest; its four waves take the four quarters of the rows' key tiles. A sequence
-    // with more rows than row_blocks blocks has its later blocks taken in turn.
+    // decode and verify: workgroup = (kv head, key piece, 16-row block, sequence), kv head
+    // fastest; its four waves take the four quarters of its piece of the rows' key tiles.
+    // A sequence with more rows than row_blocks blocks has its later blocks taken in turn
+    // (verify, whose calls have one piece).
     const int64_t item = blockIdx.x;
     const int h = (int)(item % a.hkv);
     const int64_t rest = item / a.hkv;
-    const int b = (int)(rest / a.row_blocks);
-    const int rb = (int)(rest - (int64_t)b * a.row_blocks);
+    const int piece = (int)(rest % a.pieces);
+    const int64_t blk_item = rest / a.pieces;
+    const int b = (int)(blk_item / a.row_blocks);
+    const int rb = (int)(blk_item - (int64_t)b * a.row_blocks);
     if (b >= a.batch) return;
+    piece_slot = (blk_item * a.hkv + h) * a.pieces + piece;
     int rows_b;
     if (a.qsl) rows_b = clamp_query_rows(cptr(a.qsl)[b], cptr(a.qsl)[b + 1], a.num_tokens).ntok * a.group;
     else rows_b = (b < a.num_tokens ? 1 : 0) * a.group;
 #pragma unroll 1
-    for (int r0 = rb * kAnyRows; r0 < rows_b; r0 += a.row_blocks * kAnyRows) rows(AnyMode<false>{}, b, h, r0, wave);
+    for (int r0 = rb * kAnyRows; r0 < rows_b; r0 += a.row_blocks * kAnyRows)
+      rows(AnyMode<false>{}, b, h, r0, piece * kAnyWaves + wave);
+  }
+}
+
+// Merge of the key pieces of a decode (pieces > 1): one workgroup per (sequence, 16-row
+// block, kv head), 16 threads per row, each thread four dims of every 64. The row's 16
+// threads read the pieces' log2 LSEs 16 at a time and reduce them across lanes, so every
+// load of a round is in flight together; a piece's weight is 2^(lse - max), and its O
+// chunks are then read eight pieces at a time. Pieces that saw no key have weight 0.
+template <int DP, bool QBF16>
+__global__ __launch_bounds__(256) void any_merge(const AnyArgs args) {
+  const AnyArgs a = args;
+  constexpr int kNC = DP / 64;  // f32x4 chunks per thread
+  const int item = (int)blockIdx.x;  // (b * row_blocks + rb) * hkv + h
+  const int h = item % a.hkv;
+  const int blk_item = item / a.hkv;
+  const int b = blk_item / a.row_blocks;
+  const int rb = blk_item - b * a.row_blocks;
+  const int row = threadIdx.x >> 4;
+  const int part = threadIdx.x & 15;
+  const int lane16 = (threadIdx.x & 63) & ~15;  // first lane of this row's 16 in the wave
+  const int R = rb * kAnyRows + row;  // decode: rows 0 .. G-1 of one token
+  // the row's 16 threads stay together (rows are whole 16-lane groups of a wave)
+  const bool live = b < a.batch && b < a.num_tokens && R < a.group;
+  const int np = a.pieces;
+  const int64_t slot0 = (int64_t)item * np;
+  const float MA_GLOBAL* lse = gptr(a.part_lse) + slot0 * 16 + row;
+  const float MA_GLOBAL* po = gptr(a.part_o) + slot0 * (16 * DP) + row * DP + part * 4;
+  // 1. max LSE over the pieces: thread `part` reads pieces part, part + 16, ...
+  float lv[4];  // up to 64 pieces per row in registers
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int p = part + 16 * k;
+    lv[k] = (live && p < np) ? lse[(int64_t)p * 16] : -INFINITY;
+    m = fmaxf(m, lv[k]);
+  }
+  for (int p = part + 64; p < np; p += 16) m = fmaxf(m, live ? lse[(int64_t)p * 16] : -INFINITY);
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  // 2. weights of this thread's pieces and their sum over the row
+  float wv[4];
+  float wsum = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    wv[k] = (lv[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(lv[k] - m);
+    wsum += wv[k];
+  }
+  for (int p = part + 64; p < np; p += 16) {
+    const float l = live ? lse[(int64_t)p * 16] : -INFINITY;
+    wsum += (l == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(l - m);
+  }
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1) wsum += __shfl_xor(wsum, d, 64);
+  // 3. the weighted sum of the pieces' O, eight pieces' loads in flight at a time
+  f32x4 acc[kNC];
+#pragma unroll
+  for (int x = 0; x < kNC; ++x) acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (live && wsum > 0.f) {
+    for (int p0 = 0; p0 < np; p0 += 8) {
+      f32x4 ov[8][kNC];
+      float w8[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int p = p0 + u;
+        // the weight of piece p sits in lane (p % 16) of the row's group, register p / 16
+        const int k = (p >> 4) & 3;
+        const float wk = k == 0 ? wv[0] : k == 1 ? wv[1] : k == 2 ? wv[2] : wv[3];
+        float w = __shfl(wk, lane16 + (p & 15), 64);
+        if (p >= 64) {
+          const float l = p < np ? lse[(int64_t)p * 16] : -INFINITY;
+          w = (l == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(l - m);
+        }
+        w8[u] = p < np ? w : 0.f;
+#pragma unroll
+        for (int x = 0; x < kNC; ++x)
+          ov[u][x] = (p < np && w8[u] > 0.f)
+                         ? *reinterpret_cast<const f32x4 MA_GLOBAL*>(po + (int64_t)p * (16 * DP) + x * 64)
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int x = 0; x < kNC; ++x) acc[x] += ov[u][x] * w8[u];
+    }
+  }
+  if (!live) return;
+  const float inv = (wsum > 0.f) ? a.v_scale / wsum : 0.f;
+  const int g = R;
+  const int64_t off = (int64_t)b * a.out_stride_tok + (int64_t)(h * a.group + g) * a.out_stride_head;
+#pragma unroll
+  for (int x = 0; x < kNC; ++x) {
+    const int d0 = x * 64 + part * 4;
+    if (d0 < a.head_dim) store_out4<QBF16>(a.out, off + d0, acc[x], inv, a.out_f32);
   }
 }
 
@@ -733,7 +849,12 @@ static hipError_t launch_any_q(int kv, dim3 grid, hipStream_t st, const AnyArgs&
 
 template <int DP>
 static hipError_t launch_any_d(bool qbf16, int kv, dim3 grid, hipStream_t st, const AnyArgs& a) {
-  return qbf16 ? launch_any_q<DP, true>(kv, grid, st, a) : launch_any_q<DP, false>(kv, grid, st, a);
+  hipError_t e = qbf16 ? launch_any_q<DP, true>(kv, grid, st, a) : launch_any_q<DP, false>(kv, grid, st, a);
+  if (e != hipSuccess || a.pieces <= 1) return e;
+  const dim3 mgrid(grid.x / (unsigned)a.pieces);
+  if (qbf16) hipLaunchKernelGGL((any_merge<DP, true>), mgrid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((any_merge<DP, false>), mgrid, dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 hipError_t any_launch(const AnyArgs& a, int q_dtype, int kv_dtype, int64_t grid_x, hipStream_t st) {

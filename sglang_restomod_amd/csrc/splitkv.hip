@@ -48,6 +48,7 @@
 // at the wave's last tile, so the pipelined loop has no data-dependent branches around
 // loads and the counts stay exact.
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -962,11 +963,29 @@ static constexpr size_t ws_bytes(int num_workgroups, int head_dim) {
          (((size_t)num_workgroups * kWaves * 2 * kMaxRows * sizeof(float) + 255) & ~(size_t)255);
 }
 
+// Decode on the any-head-dim kernel splits each row block's keys over up to this many
+// workgroups per compute unit in all (the piece partials the workspace holds).
+constexpr int kPieceWgPerCu = 2;
+
 extern "C" size_t ma_splitkv_workspace_bytes(int num_workgroups, int head_dim) {
   if (num_workgroups <= 0 || head_dim <= 0) return 0;
-  if (any_head_dim(head_dim)) return 0;  // the any-head-dim kernel keeps no partials
+  // the any-head-dim kernel keeps only the pieces of a split decode
+  if (any_head_dim(head_dim)) return any_piece_bytes((int64_t)num_workgroups * kPieceWgPerCu, head_dim);
   return ws_bytes(num_workgroups, head_dim);
 }
+
+// A decode whose split-KV tile count (32-key tiles over every sequence, kv head and row
+// group, at the longest length the caller knows) is at most this runs on the any-head-dim
+// kernel as one pass over key pieces plus a merge: for so little work the persistent
+// kernel's start (a scan of every sequence) and its merge over every wave's descriptor
+// cost more than they save. Measured at D = 128, 32 / 8 heads, B 1-32 and contexts of
+// 512-8192: the pieces are faster up to 16384 tiles (B = 8 at 8192 keys: 51.8 against
+// 61.5 us per call; B = 32 at 2048: 45.6 against 59.4) and slower beyond (B = 16 at 8192:
+// 110 against 101); B = 1 at 512 keys takes 16.5 us per call either way.
+#ifndef MA_SMALL_DECODE_TILES
+#define MA_SMALL_DECODE_TILES 16384
+#endif
+constexpr int64_t kSmallDecodeTiles = MA_SMALL_DECODE_TILES;
 
 // ---------------------------------------------------------------------------
 // Static scratch of the allocation-free decode (ma_grouped_decode_noalloc): the split-KV
@@ -1007,7 +1026,8 @@ static int scratch_of_current_device(void** out) {
 extern "C" int ma_device_workgroups(void) { return device_workgroups(0); }
 
 static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, int max_q_per_seq,
-                       int num_workgroups, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                       int num_workgroups, int max_seq_len, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
   const bool generic = any_head_dim(head_dim);  // served by the any-head-dim kernel
   if (!generic && head_dim != 64 && head_dim != 128 && head_dim != 256)
     return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (multiples of 16 up to %d)", head_dim, kAnyMaxDim);
@@ -1037,9 +1057,20 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
   a.group = a.hq / a.hkv;
   if ((int64_t)a.num_tokens * a.group > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens x GQA group exceeds 2^31");
-  if (generic) {
-    // no workspace: one workgroup per 16 rows (token, GQA head), its four waves splitting
-    // the keys and merging through LDS
+  if (max_seq_len < 0) return set_error(MA_EINVAL, "max_seq_len must be >= 0 (0: not known)");
+  const bool decode = a.qsl == nullptr;
+  // a small decode: the split-KV tiles at the longest length the caller knows
+  bool small = false;
+  if (!generic && decode && max_seq_len > 0) {
+    const int rows_total = a.group;
+    const int64_t row_groups = (rows_total + 31) / 32;
+    const int64_t tiles = (int64_t)a.batch * a.hkv * row_groups * ((max_seq_len + 31) / 32);
+    small = tiles <= kSmallDecodeTiles;
+  }
+  if (generic || small) {
+    // one workgroup per 16 rows (token, GQA head), its four waves splitting the keys and
+    // merging through LDS; a decode also splits each row block's keys over `pieces`
+    // workgroups when the grid would leave compute units idle, merged by a second kernel
     AnyArgs g{};
     g.q = a.q; g.q_stride_tok = a.q_stride_tok; g.q_stride_head = a.q_stride_head;
     g.k = a.k; g.v = a.v; g.kv_stride_row = a.kv_stride_row; g.kv_stride_head = a.kv_stride_head;
@@ -1049,7 +1080,27 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
     g.row_blocks = (int)(((int64_t)max_q_per_seq * a.group + kAnyRows - 1) / kAnyRows);
     g.causal = a.causal; g.window = a.window; g.scale_log2 = a.scale_log2; g.v_scale = a.v_scale;
     g.out = a.out; g.out_stride_tok = a.out_stride_tok; g.out_stride_head = a.out_stride_head; g.out_f32 = a.out_f32;
-    const int64_t grid = (int64_t)a.batch * a.hkv * g.row_blocks;  // one workgroup per row block
+    g.pieces = 1;
+    const int64_t base = (int64_t)a.batch * a.hkv * g.row_blocks;  // one workgroup per row block
+    const int64_t cap_slots = (int64_t)num_workgroups * kPieceWgPerCu;
+    if (decode && base < num_workgroups && workspace && workspace_bytes >= any_piece_bytes(cap_slots, head_dim) &&
+        !(reinterpret_cast<uintptr_t>(workspace) & 255)) {
+      // pieces: enough workgroups to cover the chip twice, no more than one 16-key tile per
+      // wave at the longest length known (the caller's bound, else the table's width),
+      // within the workspace's piece slots; each piece is an equal share of its sequence's
+      // own keys, so any bound gives the same result
+      const int64_t width = max_seq_len > 0 ? (int64_t)max_seq_len : (a.tt.stride << a.tt.page_shift);
+      const int64_t by_len = (width + kAnyWaves * kAnyKeys - 1) / (kAnyWaves * kAnyKeys);
+      const int64_t want = (cap_slots + base - 1) / base;
+      const int64_t pieces = std::min(std::min(want, by_len), cap_slots / base);
+      if (pieces > 1) {
+        g.pieces = (int)pieces;
+        char* ws = reinterpret_cast<char*>(workspace);
+        g.part_o = reinterpret_cast<float*>(ws);
+        g.part_lse = reinterpret_cast<float*>(ws + any_piece_o_bytes(cap_slots, head_dim));
+      }
+    }
+    const int64_t grid = base * g.pieces;
     if (grid > 0x7fffffff) return set_error(MA_EINVAL, "grid too large");
     const hipError_t e = any_launch(g, q_dtype, kv_dtype, grid, stream);
     if (e != hipSuccess) return set_error(MA_ELAUNCH, "any-head-dim launch failed: %s", hipGetErrorString(e));
@@ -1089,7 +1140,7 @@ extern "C" int ma_grouped_decode(
     const int32_t* table, int64_t table_stride, const int64_t* row_index, int page_size,
     const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
     int num_workgroups, float softmax_scale, float k_scale, float v_scale,
-    int sliding_window, void* workspace, size_t workspace_bytes,
+    int sliding_window, int max_seq_len, void* workspace, size_t workspace_bytes,
     void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
   if (page_size <= 0 || (page_size & (page_size - 1))) return set_error(MA_EINVAL, "page size %d must be a power of two", page_size);
   if ((q_dtype == DT_F16 || q_dtype == DT_BF16) && out_dtype != q_dtype && out_dtype != DT_F32)
@@ -1105,7 +1156,7 @@ extern "C" int ma_grouped_decode(
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
   a.out_f32 = out_dtype == DT_F32;
-  return splitkv_run(a, head_dim, q_dtype, kv_dtype, 1, num_workgroups, workspace, workspace_bytes,
+  return splitkv_run(a, head_dim, q_dtype, kv_dtype, 1, num_workgroups, max_seq_len, workspace, workspace_bytes,
                      (hipStream_t)stream);
 }
 
@@ -1135,7 +1186,7 @@ extern "C" int ma_paged_verify(
   a.scale_log2 = softmax_scale * k_scale * kLog2e; a.v_scale = v_scale;
   a.out = out; a.out_stride_tok = out_stride_tok; a.out_stride_head = out_stride_head;
   a.out_f32 = out_dtype == DT_F32;
-  return splitkv_run(a, head_dim, q_dtype, kv_dtype, max_q_per_seq, num_workgroups, workspace, workspace_bytes,
+  return splitkv_run(a, head_dim, q_dtype, kv_dtype, max_q_per_seq, num_workgroups, 0, workspace, workspace_bytes,
                      (hipStream_t)stream);
 }
 
@@ -1145,15 +1196,17 @@ extern "C" int ma_grouped_decode_noalloc(
     const int32_t* table, int64_t table_stride, const int64_t* row_index, int page_size,
     const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
     int num_workgroups, float softmax_scale, float k_scale, float v_scale, int sliding_window,
-    void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
+    int max_seq_len, void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_head, void* stream) {
   if (num_workgroups <= 0 || num_workgroups > kScratchWorkgroups)
     return set_error(MA_EINVAL, "num_workgroups %d: the static scratch serves 1..%d", num_workgroups, kScratchWorkgroups);
-  // head dims above 256 run on the any-head-dim kernel, which uses no scratch
+  // the scratch holds the split-KV workspace of the largest grid at head dim 256, which also
+  // covers the key pieces of the any-head-dim kernel at every head dim up to 512
+  static_assert(any_piece_bytes_c(kScratchWorkgroups * kPieceWgPerCu, 512) <= kScratchBytes, "scratch too small");
   void* ws = nullptr;
   const int rc = scratch_of_current_device(&ws);
   if (rc != MA_OK) return rc;
   return ma_grouped_decode(q, q_stride_tok, q_stride_head, q_dtype, k_cache, v_cache, kv_stride_row, kv_stride_head,
                            kv_dtype, table, table_stride, row_index, page_size, seq_lens, batch, num_q_heads,
-                           num_kv_heads, head_dim, num_workgroups, softmax_scale, k_scale, v_scale, sliding_window, ws,
-                           kScratchBytes, out, out_dtype, out_stride_tok, out_stride_head, stream);
+                           num_kv_heads, head_dim, num_workgroups, softmax_scale, k_scale, v_scale, sliding_window,
+                           max_seq_len, ws, kScratchBytes, out, out_dtype, out_stride_tok, out_stride_head, stream);
 }

@@ -54,7 +54,7 @@ def test_abi_version(lib):
 def _decode_args(**over):
     args = dict(q=1 << 20, qs0=1024, qs1=128, qdt=1, k=1 << 21, v=1 << 22, rs=1024, hs=128, kvdt=1,
                 table=1 << 23, tstride=64, rowidx=None, ps=1, seq=1 << 24, batch=2, hq=8, hkv=8, dim=128,
-                nwg=4, sm=0.1, ks=1.0, vs=1.0, win=-1, ws=None, wsb=0,
+                nwg=4, sm=0.1, ks=1.0, vs=1.0, win=-1, msl=0, ws=None, wsb=0,
                 out=1 << 25, odt=1, os0=1024, os1=128, stream=None)
     args.update(over)
     return list(args.values())
@@ -74,6 +74,7 @@ def _decode_args(**over):
     ({"nwg": 0}, "num_workgroups"),
     ({"odt": 2}, "out dtype"),
     ({"odt": 4, "os1": 130}, "aligned"),
+    ({"msl": -1}, "max_seq_len"),
 ])
 def test_bad_arguments_are_rejected_before_launch(lib, over, msg):
     status = lib.ma_grouped_decode(*_decode_args(**over))
@@ -87,12 +88,16 @@ def test_empty_batch_is_a_no_op(lib):
 
 def test_workspace_size_formula(lib):
     assert lib.ma_splitkv_workspace_bytes(0, 128) == 0
-    # the other head dims run on a kernel without a workspace
-    for d in (16, 96, 192, 320, 512):
-        assert lib.ma_splitkv_workspace_bytes(256, d) == 0
+    # the other head dims hold only the key pieces of a split decode: two per compute unit,
+    # 16 rows each, at the kernel's padded width (O) plus one LSE per row
+    for d, dp in ((16, 64), (96, 128), (192, 256), (320, 512), (512, 512)):
+        n = lib.ma_splitkv_workspace_bytes(256, d)
+        assert n == 512 * 16 * dp * 4 + 512 * 16 * 4, d
     n = lib.ma_splitkv_workspace_bytes(256, 128)
     # two partial pieces of up to 32 rows per wave, 4 waves per workgroup
     assert n >= 256 * 4 * 2 * 32 * 129 * 4 and n % 256 == 0
+    # which also hold the pieces of a small decode routed to the any-head-dim kernel
+    assert n >= 512 * 16 * 128 * 4 + 512 * 16 * 4
 
 
 def _kvw_args(**over):
@@ -214,3 +219,17 @@ def test_loader_constants_match_the_header():
     for name in ("MA_OK", "MA_EINVAL", "MA_ELAUNCH", "MA_EUNSUPPORTED", "MA_NOALLOC_MAX_WORKGROUPS"):
         want = int(re.search(rf"#define {name} \(?(-?\d+)\)?", hdr).group(1))
         assert getattr(L, name) == want, name
+
+
+def test_small_decode_rule_matches_the_library():
+    """ops.decode_kernel mirrors the library's routing constant and rule."""
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    src = open(os.path.join(ROOT, "sglang_restomod_amd", "csrc", "splitkv.hip")).read()
+    assert int(re.search(r"#define MA_SMALL_DECODE_TILES (\d+)", src).group(1)) == ops.SMALL_DECODE_TILES
+    assert ops.decode_kernel(1, 32, 8, 128, 512) == "any_kernel"          # 8 x 16 tiles
+    assert ops.decode_kernel(1, 32, 8, 128, None) == "splitkv_partial"    # no bound: persistent
+    assert ops.decode_kernel(64, 64, 8, 128, 8192) == "splitkv_partial"
+    assert ops.decode_kernel(64, 16, 4, 512, 8192) == "any_kernel"        # not a tuned head dim
+    assert ops.decode_kernel(8, 64, 8, 128, 8192) == "any_kernel"         # 8 x 8 x 256 = 16384 tiles
+    assert ops.decode_kernel(8, 64, 8, 128, 8193) == "splitkv_partial"

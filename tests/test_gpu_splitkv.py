@@ -261,21 +261,25 @@ def test_verify_ragged_query_counts(gpu):
     assert_attn_close(out, ref, what="ragged verify")
 
 
-@pytest.mark.parametrize("mode", ["decode", "verify"])
+@pytest.mark.parametrize("mode", ["decode", "decode_pieces", "verify"])
 def test_poisoned_workspace_and_output(gpu, mode):
     """The workspace needs no initialisation: filled with 0xFF bytes (NaN pieces, -1
     descriptors) and reused by a smaller call, and with the output pre-filled with NaN,
-    every result is the one a fresh workspace gives, bit for bit."""
+    every result is the one a fresh workspace gives, bit for bit. decode_pieces: the small
+    decode split over key pieces (a length bound given), whose pieces live there too."""
     ops = _ops()
-    idx = 1 if mode == "decode" else 4
-    big = workloads.make(idx, device=gpu, batch=12, scale_lens=0.3)
-    small = workloads.make(idx, device=gpu, batch=3, scale_lens=0.05)
+    idx = 4 if mode == "verify" else 1
+    big = workloads.make(idx, device=gpu, batch=12 if mode != "decode_pieces" else 2, scale_lens=0.3)
+    small = workloads.make(idx, device=gpu, batch=3 if mode != "decode_pieces" else 1, scale_lens=0.05)
 
     def run(w, ws, out):
-        if mode == "decode":
+        if mode.startswith("decode"):
+            hint = max(w.seq_lens_cpu) if mode == "decode_pieces" else None
+            if hint is not None:
+                assert ops.decode_kernel(w.batch, w.heads, w.heads_kv, w.dim, hint) == "any_kernel"
             return ops.grouped_decode_forward(
                 w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, softmax_scale=w.softmax_scale,
-                row_index=w.req_pool_indices, out=out, workspace=ws)
+                row_index=w.req_pool_indices, out=out, workspace=ws, max_seq_len_hint=hint)
         T = int(w.extend_lens[0])
         return ops.paged_verify_forward(
             w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, w.query_start_loc, w.prefix_lens,

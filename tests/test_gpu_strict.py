@@ -32,12 +32,14 @@ def _ops():
     return ops
 
 
-def _call(w, out):
+def _call(w, out, hint=False):
     ops = _ops()
     if w.mode == "decode":
+        # hint: the host-known longest length, which sends a small decode to the key pieces
         return ops.grouped_decode_forward(w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens,
                                           softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale,
-                                          out=out, row_index=w.req_pool_indices)
+                                          out=out, row_index=w.req_pool_indices,
+                                          max_seq_len_hint=max(w.seq_lens_cpu) if hint else None)
     qsl = w.query_start_loc
     if w.mode == "verify":
         return ops.paged_verify_forward(w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, qsl, w.prefix_lens,
@@ -55,20 +57,22 @@ def _half_ulp(ref: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return 0.5 * torch.exp2(torch.floor(torch.log2(mag)) - mant)
 
 
-CASES = [(0, "e4m3"), (1, "e4m3"), (3, "e4m3"), (3, "e5m2"), (4, "e4m3"), (2, "e4m3"), (5, "e4m3"), (6, "e4m3"),
-         (7, "e4m3"), (8, "e4m3"), (9, "e4m3"), (10, "e4m3"), (11, "e4m3"), (11, "e5m2")]
+CASES = [(0, "e4m3", False), (0, "e4m3", True), (1, "e4m3", False), (1, "e4m3", True), (3, "e4m3", False),
+         (3, "e5m2", False), (4, "e4m3", False), (2, "e4m3", False), (5, "e4m3", False), (6, "e4m3", False),
+         (7, "e4m3", False), (8, "e4m3", False), (9, "e4m3", False), (10, "e4m3", False), (11, "e4m3", False),
+         (11, "e5m2", False)]
 
 
-@pytest.mark.parametrize("index,fmt", CASES)
-def test_every_output_at_full_size(index, fmt):
+@pytest.mark.parametrize("index,fmt,hint", CASES)
+def test_every_output_at_full_size(index, fmt, hint):
     w = workloads.make(index, device=DEV, kv_format=fmt)
-    tag = w.name + (f"_{fmt}" if w.kv_format else "")
+    tag = w.name + (f"_{fmt}" if w.kv_format else "") + ("_hinted" if hint else "")
     print(f"[case] strict {tag}: {w.batch} sequences, {w.q.shape[0]} query rows", flush=True)
     slots = F64.rows_of_table(w.req_to_token, w.req_pool_indices, w.seq_lens_cpu)
     ref = F64.attend(w.q, w.k_pool, w.v_pool, slots, w.query_start_loc.tolist(), w.prefix_lens.tolist(),
                      w.seq_lens_cpu, softmax_scale=w.softmax_scale, k_scale=w.k_scale, v_scale=w.v_scale)
-    out32 = _call(w, torch.empty(w.q.shape, dtype=torch.float32, device=DEV))
-    out16 = _call(w, torch.empty_like(w.q))
+    out32 = _call(w, torch.empty(w.q.shape, dtype=torch.float32, device=DEV), hint)
+    out16 = _call(w, torch.empty_like(w.q), hint)
     torch.cuda.synchronize()
     assert torch.isfinite(out32).all() and torch.isfinite(out16).all()
     err32 = (out32.double() - ref).abs()

@@ -29,7 +29,8 @@ def _args(w, out, nwg):
                  k.data_ptr(), v.data_ptr(), row, head, ops.kv_dtype_code(k.dtype),
                  w.req_to_token.data_ptr(), w.req_to_token.stride(0), ridx.data_ptr(), ps,
                  seq.data_ptr(), w.batch, w.heads, hkv, dim, nwg,
-                 ctypes.c_float(w.softmax_scale), ctypes.c_float(w.k_scale), ctypes.c_float(w.v_scale), -1)
+                 ctypes.c_float(w.softmax_scale), ctypes.c_float(w.k_scale), ctypes.c_float(w.v_scale), -1,
+                 max(w.seq_lens_cpu))
     tail = (out.data_ptr(), ops.q_dtype_code(out.dtype), out.stride(0), out.stride(1), stream)
     return head_args, tail, (seq, ridx)
 
