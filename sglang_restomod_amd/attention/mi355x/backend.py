@@ -77,6 +77,9 @@ class MI355XForwardMetadata:
     num_tokens: int = 0
     swa_table: Optional[torch.Tensor] = None
     swa_row_index: Optional[torch.Tensor] = None
+    # the longest sequence when the host knows it (eager forwards), else 0: it only picks
+    # the decode kernels, never the result
+    max_seq_len: int = 0
 
 
 def _mode_is(mode, name: str) -> bool:
@@ -127,6 +130,7 @@ class MI355XAttnBackend(_EngineBase):
         self._cg_query_start_loc: Optional[torch.Tensor] = None
         self._cg_prefix_kv_lens: Optional[torch.Tensor] = None
         self._cg_swa_table: Optional[torch.Tensor] = None
+        self._cg_rows_per_req = 0  # rows per request of the captured draft-extend graphs
 
     # ------------------------------------------------------------------
     # Mode routing (reference: _uses_native_linear_verify :332-380,
@@ -177,6 +181,8 @@ class MI355XAttnBackend(_EngineBase):
         row_index = req_pool_indices.to(torch.int64)
         seq = seq_lens.to(torch.int32)
         md = MI355XForwardMetadata(mode=mode, table=self.req_to_token, row_index=row_index, seq_lens=seq)
+        if seq_lens_cpu is not None and len(seq_lens_cpu):
+            md.max_seq_len = max(0, int(max(int(x) for x in seq_lens_cpu)))
         if mode != MODE_DECODE:
             ext = extend_seq_lens.to(torch.int32)
             pre = extend_prefix_lens.to(torch.int32)
@@ -300,12 +306,23 @@ class MI355XAttnBackend(_EngineBase):
                 torch.arange(0, (bs + 1) * n, n, dtype=torch.int32, device=seq.device))
             mode, max_q = MODE_VERIFY, n
         elif _mode_is(forward_mode, "is_draft_extend_v2") or _mode_is(forward_mode, "is_draft_extend"):
-            # the graph API carries neither the prefix nor the rows of each request, and the
-            # engine's per-request row counts in a captured draft extend are not pinned here
-            # (the reference hands these graphs to another backend, :747, :801)
-            raise NotImplementedError(
-                "mi355x_attn does not capture draft-extend graphs (per-request rows are not part of the "
-                "capture/replay arguments); run the draft extend eagerly")
+            # a captured draft extend runs a fixed number of rows per request (the graph's
+            # num_tokens / bs, the layout graph runners pad to): request b's rows are the
+            # last n positions of its seq_lens[b] keys. Built on the device in the fixed
+            # buffers, so a replay only refreshes them. (The reference hands these graphs to
+            # another backend, :747, :801.)
+            if bs <= 0 or num_tokens % bs:
+                raise NotImplementedError(
+                    f"a captured draft extend needs the same number of rows per request ({num_tokens} tokens "
+                    f"over {bs} requests)")
+            n = int(num_tokens) // bs
+            self._cg_rows_per_req = n
+            self._cg_seq_lens[:bs].copy_(seq)
+            torch.sub(seq, n, out=self._cg_prefix_kv_lens[:bs])
+            self._cg_prefix_kv_lens[:bs].clamp_(min=0)
+            self._cg_query_start_loc[: bs + 1].copy_(
+                torch.arange(0, (bs + 1) * n, n, dtype=torch.int32, device=seq.device))
+            mode, max_q = (MODE_VERIFY, n) if n <= ops.VERIFY_MAX_Q_PER_SEQ else (MODE_EXTEND, n)
         else:
             # captured extend: the tokens of each sequence are all new (the reference
             # approximates the same way, :838-843); the grid covers num_tokens rows
@@ -332,6 +349,9 @@ class MI355XAttnBackend(_EngineBase):
                                                 encoder_lens, forward_mode, spec_info,
                                                 seq_lens_cpu=None) -> None:
         num_tokens = self.forward_metadata.num_tokens if self.forward_metadata is not None else bs
+        draft = _mode_is(forward_mode, "is_draft_extend_v2") or _mode_is(forward_mode, "is_draft_extend")
+        if draft and self.forward_metadata is not None and self._cg_rows_per_req:
+            num_tokens = bs * self._cg_rows_per_req
         if _mode_is(forward_mode, "is_target_verify"):
             num_tokens = bs * int(spec_info.draft_token_num)
         elif _mode_is(forward_mode, "is_decode_or_idle"):
@@ -418,7 +438,8 @@ class MI355XAttnBackend(_EngineBase):
             ops.grouped_decode_forward(
                 q3, k_cache, v_cache, table, md.seq_lens, softmax_scale=float(layer.scaling),
                 k_scale=ks, v_scale=vs, out=out, row_index=rows, page_size=1,
-                sliding_window_size=window, workspace=self.splitkv_workspace())
+                sliding_window_size=window, max_seq_len_hint=md.max_seq_len,
+                workspace=self.splitkv_workspace())
         out = out.reshape(q3.shape[0], hq * d)
         return out if out.dtype == out_dtype else out.to(out_dtype)
 

@@ -64,16 +64,21 @@ class DraftRows:
     row_index: Optional[torch.Tensor]
     lens: torch.Tensor  # [passes, rows] int32
     swa_table: Optional[torch.Tensor] = None
+    swa_row_index: Optional[torch.Tensor] = None  # row of swa_table per query row (None: row r)
+    max_len: int = 0  # the longest row when the host knows it (eager rounds), else 0
 
     @property
     def rows(self) -> int:
         return int(self.lens.shape[1])
 
     @staticmethod
-    def from_flat_lists(kv_indptr: torch.Tensor, kv_indices: torch.Tensor) -> "DraftRows":
+    def from_flat_lists(kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                        swa_mapping: Optional[torch.Tensor] = None) -> "DraftRows":
         """One pass whose rows come as a flat list (row ``r`` owns
         ``kv_indices[kv_indptr[r]:kv_indptr[r+1]]``): read in place as a table of row
-        stride 1 with row starts ``kv_indptr[:-1]``."""
+        stride 1 with row starts ``kv_indptr[:-1]``. With an SWA pool's slot mapping
+        (full-pool slot -> SWA slot), the list is also translated, on the device, for
+        the pool's sliding-window layers."""
         if kv_indices.dtype != torch.int32:
             raise ValueError("kv_indices must be int32")
         rows = max(int(kv_indptr.numel()) - 1, 0)
@@ -81,7 +86,12 @@ class DraftRows:
         lens = (kv_indptr[1:rows + 1] - kv_indptr[:rows]).to(torch.int32).reshape(1, rows)
         base = kv_indices if kv_indices.numel() else torch.zeros(1, dtype=torch.int32, device=kv_indptr.device)
         table = torch.as_strided(base, (base.numel(), 1), (1, 1))
-        return DraftRows(table=table, row_index=starts, lens=lens)
+        swa_table = None
+        if swa_mapping is not None:
+            swa = swa_mapping[base.to(torch.int64)].to(torch.int32)
+            swa_table = torch.as_strided(swa, (swa.numel(), 1), (1, 1))
+        return DraftRows(table=table, row_index=starts, lens=lens, swa_table=swa_table,
+                         swa_row_index=starts if swa_table is not None else None)
 
 
 def support_gaps(model_runner, topk: int, draft_window=(0, 0), layers=None) -> list[str]:
@@ -136,8 +146,16 @@ class MI355XDraftDecodeBackend(_EngineBase):
 
     def use_flat_lists(self, kv_indptr: torch.Tensor, kv_indices: torch.Tensor) -> int:
         """Serve this pass from a flat index list instead of the round's rows; returns its rows."""
-        self._own = DraftRows.from_flat_lists(kv_indptr, kv_indices)
+        self._own = DraftRows.from_flat_lists(kv_indptr, kv_indices, self.container.swa_mapping)
         return self._own.rows
+
+    @staticmethod
+    def table_for(rows: DraftRows, window: int):
+        """(table, row_index) a layer reads: the SWA pool's translated rows for a
+        sliding-window layer when the pool has them, else the full pool's rows."""
+        if window >= 0 and rows.swa_table is not None:
+            return rows.swa_table, rows.swa_row_index
+        return rows.table, rows.row_index
 
     def init_forward_metadata(self, forward_batch) -> None:
         spec_info = getattr(forward_batch, "spec_info", None)
@@ -185,15 +203,14 @@ class MI355XDraftDecodeBackend(_EngineBase):
             default_causal=True, is_cross_attention=bool(getattr(layer, "is_cross_attention", False)),
             is_encoder_only=_is_encoder_only(layer), sliding_window_size=getattr(layer, "sliding_window_size", None))
         if n:
-            table, row_index = rows.table, rows.row_index
-            if window >= 0 and rows.swa_table is not None:
-                table, row_index = rows.swa_table, None
+            table, row_index = self.table_for(rows, window)
             ks = float(layer.k_scale_float) if getattr(layer, "k_scale", None) is not None else 1.0
             vs = float(layer.v_scale_float) if getattr(layer, "v_scale", None) is not None else 1.0
             ops.grouped_decode_forward(
                 q3, k_cache, v_cache, table, rows.lens[0 if self._own is not None else self.step],
                 softmax_scale=float(layer.scaling), k_scale=ks, v_scale=vs, out=out, row_index=row_index,
-                page_size=1, sliding_window_size=window, workspace=self.container.workspace(d))
+                page_size=1, sliding_window_size=window, max_seq_len_hint=rows.max_len,
+                workspace=self.container.workspace(d))
         out = out.reshape(n, hq * d)
         return out if out.dtype == q.dtype else out.to(q.dtype)
 
@@ -242,6 +259,9 @@ class MI355XMultiStepDraftBackend:
         self.current: Optional[DraftRows] = None
         self._ws: Optional[torch.Tensor] = None
         self._graph: Optional[dict] = None
+        # eager rounds write their tables into these (grown as needed, reused every round:
+        # the passes of one round run before the next round's table on the same stream)
+        self._eager: dict = {}
 
     # ---- buffers ----
     def workspace(self, head_dim: int) -> torch.Tensor:
@@ -257,6 +277,17 @@ class MI355XMultiStepDraftBackend:
 
     def _needs_table(self) -> bool:
         return self.topk > 1
+
+    def _eager_buffer(self, name: str, rows: int, width: int) -> torch.Tensor:
+        """A [rows, width] int32 view of the container's own buffer ``name`` for an eager
+        round, grown (never shrunk) when a round needs more rows or a wider row."""
+        buf = self._eager.get(name)
+        if buf is None or buf.shape[0] < rows or buf.shape[1] < width:
+            r = max(rows, buf.shape[0] if buf is not None else 0)
+            w = max(width, buf.shape[1] if buf is not None else 0)
+            buf = torch.empty(r, w, dtype=torch.int32, device=self.device)
+            self._eager[name] = buf
+        return buf[:rows, :width]
 
     def init_cuda_graph_state(self, max_bs: int, max_num_tokens: int = 0, kv_indices_buf=None,
                               cuda_graph_num_kv_splits_buf=None) -> None:
@@ -279,6 +310,7 @@ class MI355XMultiStepDraftBackend:
              seq_lens_cpu=None, graph: bool = False) -> DraftRows:
         """The round's rows for ``bs`` requests (in graph buffers when ``graph``)."""
         bs = int(seq_lens.shape[0] if bs is None else bs)
+        max_len = 0
         rows = bs * self.topk
         seq = seq_lens[:bs].to(torch.int32)
         req = req_pool_indices[:bs].to(torch.int64)
@@ -298,20 +330,21 @@ class MI355XMultiStepDraftBackend:
             width = int(self.req_to_token.shape[1])
             if seq_lens_cpu is not None and len(seq_lens_cpu):
                 width = min(width, int(max(int(s) for s in seq_lens_cpu[:bs])) + self.speculative_num_steps)
+                max_len = width
         for i in range(self.passes):
             torch.add(per_row, i + 1, out=lens[i])
         table, row_index = self.req_to_token, req
         if self._needs_table():
-            out = self._graph["table"][:rows] if graph else None
+            out = self._graph["table"][:rows] if graph else self._eager_buffer("table", rows, width)
             table = ops.draft_table(self.req_to_token, seq, self.topk, self.speculative_num_steps, row_index=req,
                                     out=out, width=width)
             row_index = None
         swa = None
         if self.swa_mapping is not None:
-            out = self._graph["swa"][:rows] if graph else None
+            out = self._graph["swa"][:rows] if graph else self._eager_buffer("swa", rows, width)
             swa = ops.draft_table(self.req_to_token, seq, self.topk, self.speculative_num_steps, row_index=req,
                                   mapping=self.swa_mapping, out=out, width=width)
-        rows_md = DraftRows(table=table, row_index=row_index, lens=lens, swa_table=swa)
+        rows_md = DraftRows(table=table, row_index=row_index, lens=lens, swa_table=swa, max_len=max_len)
         self.current = rows_md
         for child in self.attn_backends:
             child._own = None

@@ -132,15 +132,31 @@ class Layer:
 
 
 class Engine:
-    """A model runner plus a slot allocator over a shuffled token pool."""
+    """A model runner plus a slot allocator over a shuffled token pool.
+
+    At ``page_size`` 1 every token takes a random free slot. At a larger page size the
+    pool is cut into pages of ``page_size`` consecutive slots, handed out in random order,
+    and position ``p`` of a request lives at offset ``p % page_size`` of the request's page
+    ``p // page_size`` (SGLang's paged allocator); ``req_to_token`` still holds one slot
+    per token. Page 0 holds the padding slot 0 and is never handed out.
+    """
 
     def __init__(self, device, *, hq=8, hkv=2, head_dim=128, kv_dtype=torch.bfloat16, pool_size=4096,
                  max_reqs=16, context_len=2048, layers=1, spec="NONE", topk=1, draft_worker=False,
-                 seed=0, swa=False):
+                 seed=0, swa=False, page_size=1):
         self.device = torch.device(device)
         g = torch.Generator().manual_seed(seed)
         self.gen = g
-        self.free = (torch.randperm(pool_size, generator=g) + 1).tolist()
+        self.page_size = int(page_size)
+        if self.page_size > 1:
+            if pool_size % self.page_size:
+                raise ValueError("pool_size must be a multiple of page_size")
+            pages = pool_size // self.page_size
+            # pages 1 .. pages-1 (page 0 would hold the padding slot)
+            self.free_pages = (torch.randperm(pages - 1, generator=g) + 1).tolist()
+            self.free = []
+        else:
+            self.free = (torch.randperm(pool_size, generator=g) + 1).tolist()
         swa_map = None
         if swa:
             # a second numbering of the same slots (the SWA pool of a hybrid model)
@@ -152,7 +168,7 @@ class Engine:
         self.lens = [0] * max_reqs
         self.runner = SimpleNamespace(
             device=str(self.device),
-            page_size=1,
+            page_size=self.page_size,
             model_config=SimpleNamespace(context_len=context_len, head_dim=head_dim, v_head_dim=head_dim),
             req_to_token_pool=SimpleNamespace(req_to_token=req_to_token, size=max_reqs),
             token_to_kv_pool=self.pool,
@@ -168,8 +184,20 @@ class Engine:
 
     def alloc(self, row: int, n: int) -> torch.Tensor:
         """Give request ``row`` n more tokens; returns their slots (the out_cache_loc)."""
-        slots = torch.tensor([self.free.pop() for _ in range(n)], dtype=torch.int64)
         start = self.lens[row]
+        if self.page_size > 1:
+            ps = self.page_size
+            got = []
+            for pos in range(start, start + n):
+                if pos % ps == 0:
+                    page = self.free_pages.pop()
+                else:  # the page of the previous position
+                    prev = got[-1] if got else int(self.req_to_token[row, pos - 1])
+                    page = prev // ps
+                got.append(page * ps + pos % ps)
+            slots = torch.tensor(got, dtype=torch.int64)
+        else:
+            slots = torch.tensor([self.free.pop() for _ in range(n)], dtype=torch.int64)
         self.req_to_token[row, start:start + n] = slots.to(self.device, torch.int32)
         self.lens[row] += n
         return slots.to(self.device)

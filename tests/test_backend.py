@@ -64,6 +64,33 @@ def test_decode_metadata_uses_req_to_token_in_place():
     assert md.seq_lens.dtype == torch.int32 and md.seq_lens.tolist() == [41, 18]
 
 
+def test_page_size_16_engine_places_positions_in_page_runs():
+    """The fake engine at page size 16 (the reference's production page size): position p of
+    a request lives at offset p % 16 of one page, pages are disjoint across requests, and
+    the backend builds on it with the same token-level req_to_token metadata."""
+    eng = _engine(page_size=16, pool_size=4096)
+    eng.alloc(0, 40)
+    eng.alloc(1, 5)
+    eng.alloc(0, 9)   # continues request 0's third page, then opens a fourth
+    eng.alloc(1, 30)
+    seen = set()
+    for row, n in ((0, 49), (1, 35)):
+        slots = eng.req_to_token[row, :n].tolist()
+        for p, s in enumerate(slots):
+            assert s % 16 == p % 16 and s >= 16
+            assert slots[p - p % 16] + p % 16 == s  # one page per 16 positions
+        pages = {s // 16 for s in slots}
+        assert len(pages) == -(-n // 16) and not (pages & seen)
+        seen |= pages
+    be = _backend(eng)
+    assert be.page_size == 16
+    fb = eng.batch("DECODE", [1, 0], new_tokens=[1, 1])
+    be.init_forward_metadata(fb)
+    md = be.forward_metadata
+    assert md.table is eng.req_to_token and md.seq_lens.tolist() == [36, 50]
+    assert eng.req_to_token[1, 35].item() % 16 == 35 % 16
+
+
 def test_extend_metadata():
     eng = _engine()
     eng.alloc(0, 10)  # cached prefix of request 0
@@ -152,22 +179,32 @@ def test_draft_extend_routing_reads_no_device_value():
 
 
 @pytest.mark.parametrize("mode", ["DRAFT_EXTEND", "DRAFT_EXTEND_V2"])
-def test_captured_draft_extend_is_refused(mode):
-    """The graph API does not say how many rows each request has in a draft extend; the
-    backend refuses to capture or replay one rather than guessing (a wrong guess would
-    send the kernels past q and out)."""
+def test_captured_draft_extend_uses_fixed_rows_per_request(mode):
+    """A captured draft extend runs num_tokens / bs rows per request: request b's rows are
+    the last n of its seq_lens[b] keys. Capture and replay fill the same device buffers;
+    an uneven split is refused (it has no fixed layout)."""
     eng = _engine(spec="EAGLE", draft_worker=True)
     for r in range(3):
         eng.alloc(r, 40 + r)
     be = _backend(eng)
     be.init_cuda_graph_state(max_bs=4, max_num_tokens=16)
     fm = fakes.ForwardMode(mode)
-    spec = type("S", (), {"num_tokens_per_req": 4, "draft_token_num": 4})()
+    spec = type("S", (), {"draft_token_num": 4})()
     rpi, seq = torch.tensor([0, 1, 2]), torch.tensor([40, 41, 42])
-    with pytest.raises(NotImplementedError, match="draft-extend graphs"):
-        be.init_forward_metadata_capture_cuda_graph(3, 12, rpi, seq, None, fm, spec)
-    with pytest.raises(NotImplementedError, match="draft-extend graphs"):
-        be.init_forward_metadata_replay_cuda_graph(3, rpi, seq, 123, None, fm, spec, None)
+    be.init_forward_metadata_capture_cuda_graph(3, 12, rpi, seq, None, fm, spec)
+    md = be.forward_metadata
+    assert md.mode == "verify" and md.max_q_per_seq == 4 and md.num_tokens == 12
+    assert md.query_start_loc.tolist() == [0, 4, 8, 12]
+    assert md.seq_lens.tolist() == [40, 41, 42] and md.prefix_kv_lens.tolist() == [36, 37, 38]
+    ptrs = (md.seq_lens.data_ptr(), md.prefix_kv_lens.data_ptr(), md.query_start_loc.data_ptr())
+    be.init_forward_metadata_replay_cuda_graph(3, torch.tensor([2, 0, 1]), torch.tensor([50, 44, 45]), 139,
+                                               None, fm, spec, None)
+    md = be.forward_metadata
+    assert (md.seq_lens.data_ptr(), md.prefix_kv_lens.data_ptr(), md.query_start_loc.data_ptr()) == ptrs
+    assert md.row_index.tolist() == [2, 0, 1] and md.num_tokens == 12
+    assert md.seq_lens.tolist() == [50, 44, 45] and md.prefix_kv_lens.tolist() == [46, 40, 41]
+    with pytest.raises(NotImplementedError, match="same number of rows"):
+        be.init_forward_metadata_capture_cuda_graph(3, 10, rpi, seq, None, fm, spec)
 
 
 def test_paged_forward_keeps_the_reference_signature():

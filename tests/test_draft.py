@@ -199,6 +199,48 @@ def test_flat_list_rows_are_read_in_place():
     assert [int(rows.table[int(rows.row_index[2]) + p, 0]) for p in range(3)] == [10, 11, 12]
 
 
+def test_flat_list_rows_over_an_swa_pool_translate_for_window_layers():
+    """A pass fed by a flat list over an SWA pool: sliding-window layers read the list
+    translated into SWA slots (same row starts), full-attention layers the list itself."""
+    eng, cont = _container(steps=3, swa=True)
+    mapping = eng.pool.full_to_swa_index_mapping
+    indptr = torch.tensor([0, 3, 5], dtype=torch.int32)
+    indices = torch.tensor([7, 2, 9, 4, 11], dtype=torch.int32)
+    child = cont.attn_backends[1]
+    assert child.use_flat_lists(indptr, indices) == 2
+    rows = child.rows()
+    assert rows.swa_table is not None and rows.swa_row_index.tolist() == [0, 3]
+    full_t, full_r = child.table_for(rows, -1)
+    assert full_t.data_ptr() == indices.data_ptr() and full_r.tolist() == [0, 3]
+    swa_t, swa_r = child.table_for(rows, 64)
+    assert swa_r.tolist() == [0, 3]
+    got = [int(swa_t[int(swa_r[r]) + p, 0]) for r, n in ((0, 3), (1, 2)) for p in range(n)]
+    assert got == mapping[indices.long()].tolist()
+    # a full-attention pool keeps one table for every layer
+    _, plain = _container(steps=3)
+    plain.attn_backends[0].use_flat_lists(indptr, indices)
+    r2 = plain.attn_backends[0].rows()
+    assert r2.swa_table is None and plain.attn_backends[0].table_for(r2, 64)[0].data_ptr() == indices.data_ptr()
+
+
+def test_eager_rounds_reuse_one_table_buffer():
+    """Top-k > 1 eager rounds write their rows into one container buffer, sized by the
+    longest row when the host has the lengths, and reused by later rounds."""
+    eng, cont = _container(steps=3, topk=2, context_len=2048)
+    seen = []
+    for lens in ([10, 25], [12, 27], [5, 6]):
+        fb = SimpleNamespace(req_pool_indices=torch.tensor([3, 1]), seq_lens=torch.tensor(lens), batch_size=2,
+                             seq_lens_cpu=torch.tensor(lens))
+        try:
+            cont.init_forward_metadata(fb)
+        except ValueError:  # the table kernel needs device tensors; the buffer is chosen first
+            pass
+        buf = cont._eager["table"]
+        seen.append(buf.data_ptr())
+        assert buf.shape[0] == 4 and buf.shape[1] <= max(max(x) for x in ([10, 25], [12, 27])) + 3
+    assert len(set(seen[1:])) == 1
+
+
 def test_pass_refuses_mismatched_rows():
     _, cont = _container(steps=3)
     cont.attn_backends[0].use_flat_lists(torch.tensor([0, 2], dtype=torch.int32), torch.arange(2, dtype=torch.int32))

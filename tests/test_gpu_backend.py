@@ -55,11 +55,11 @@ def _rand(gen, *shape, dtype=torch.bfloat16):
     return torch.randn(*shape, generator=gen).to(dtype).to(DEV)
 
 
-def _serving_sequence(kv_dtype, HQ=HQ, HKV=HKV, D=D):
-    print(f"[case] serving sequence {kv_dtype} hq={HQ} hkv={HKV} d={D}", flush=True)
+def _serving_sequence(kv_dtype, HQ=HQ, HKV=HKV, D=D, page_size=1):
+    print(f"[case] serving sequence {kv_dtype} hq={HQ} hkv={HKV} d={D} page_size={page_size}", flush=True)
     gen = torch.Generator().manual_seed(7)
     eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, head_dim=D, kv_dtype=kv_dtype, pool_size=12000, max_reqs=6,
-                       context_len=4096, spec="EAGLE", topk=1)
+                       context_len=4096, spec="EAGLE", topk=1, page_size=page_size)
     layer = _layer(kv_dtype, HQ, HKV, D)
     be = _backend(eng)
     # cached prefixes computed by earlier forwards
@@ -116,6 +116,14 @@ def test_serving_sequence_head_dims(kv_dtype, hq, hkv, dim):
     """The same sequence at head dims 64 and 256 (the latter with the 27B model's
     per-GPU head counts), and at 96 and 512, which run on the any-head-dim kernel."""
     _serving_sequence(kv_dtype, hq, hkv, dim)
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_serving_sequence_page_size_16(kv_dtype):
+    """The same sequence on an engine with 16-token pages (the reference's production page
+    size): every request's positions sit in runs of 16 consecutive slots, and the kernels
+    address them through the engine's token-level req_to_token."""
+    _serving_sequence(kv_dtype, page_size=16)
 
 
 def test_sliding_window_layer_through_swa_pool():
@@ -181,8 +189,12 @@ def test_decode_in_a_hip_graph_replays_with_new_lengths(HQ, HKV, D):
         graph.replay()
         torch.cuda.synchronize()
         got = out_static.clone()
-        # eager run of the same batch between replays
+        # eager runs of the same batch between replays: without the host's length bound
+        # (the kernels the graph captured, bit for bit), and with it (the eager path, which
+        # may take the key pieces)
         be.init_forward_metadata(fb)
+        hinted = be.forward_decode(q_static, None, None, layer, fb, save_kv_cache=False)
+        be.forward_metadata.max_seq_len = 0
         eager = be.forward_decode(q_static, None, None, layer, fb, save_kv_cache=False)
         torch.cuda.synchronize()
         assert torch.equal(got, eager), f"replay {step} differs from the eager call"
@@ -190,6 +202,54 @@ def test_decode_in_a_hip_graph_replays_with_new_lengths(HQ, HKV, D):
         ref = oracle.decode(to_f64(q_static).reshape(bs, HQ, D), kp, vp, eng.req_to_token.cpu().numpy(), rows,
                             fb.seq_lens.tolist(), softmax_scale=layer.scaling)
         assert_attn_close(got.reshape(bs, HQ, D), ref, what=f"graph replay {step}")
+        assert_attn_close(hinted.reshape(bs, HQ, D), ref, what=f"eager with the length bound {step}")
+
+
+@pytest.mark.parametrize("mode", ["DRAFT_EXTEND_V2", "DRAFT_EXTEND"])
+def test_draft_extend_in_a_hip_graph_replays_with_new_lengths(mode):
+    """A draft extend captured with three rows per request, replayed over grown requests:
+    every replay equals the eager call on the same batch and the float64 oracle."""
+    print(f"[case] draft extend graph {mode}", flush=True)
+    gen = torch.Generator().manual_seed(5)
+    eng = fakes.Engine(DEV, hq=HQ, hkv=HKV, kv_dtype=torch.bfloat16, pool_size=9000, max_reqs=8,
+                       context_len=4096, spec="EAGLE", draft_worker=True)
+    layer = _layer(torch.bfloat16)
+    be = _backend(eng)
+    rows, n = [5, 2, 7], 3
+    for r, p in zip(rows, [900, 40, 1700]):
+        s = eng.alloc(r, p)
+        eng.fill(0, s, _rand(gen, p, HKV, D), _rand(gen, p, HKV, D), layer)
+    bs = len(rows)
+    be.init_cuda_graph_state(max_bs=8, max_num_tokens=8 * n)
+    fb = eng.batch(mode, rows, new_tokens=[n] * bs)
+    eng.fill(0, fb.out_cache_loc, _rand(gen, bs * n, HKV, D), _rand(gen, bs * n, HKV, D), layer)
+    q_static = _rand(gen, bs * n, HQ * D)
+    be.init_forward_metadata_capture_cuda_graph(bs, bs * n, fb.req_pool_indices, fb.seq_lens, None,
+                                                fb.forward_mode, None)
+    assert be.forward_metadata.mode == "verify"
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        be.forward_extend(q_static, None, None, layer, fb, save_kv_cache=False)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_static = be.forward_extend(q_static, None, None, layer, fb, save_kv_cache=False)
+    for step in range(3):
+        if step < 2:  # the next round's rows (step 2 replays the same lengths)
+            fb = eng.batch(mode, rows, new_tokens=[n] * bs)
+            eng.fill(0, fb.out_cache_loc, _rand(gen, bs * n, HKV, D), _rand(gen, bs * n, HKV, D), layer)
+        q_static.copy_(_rand(gen, bs * n, HQ * D))
+        be.init_forward_metadata_replay_cuda_graph(bs, fb.req_pool_indices, fb.seq_lens, fb.seq_lens_sum,
+                                                   None, fb.forward_mode, None, fb.seq_lens_cpu)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out_static.clone()
+        be.init_forward_metadata(fb)
+        eager = be.forward_extend(q_static, None, None, layer, fb, save_kv_cache=False)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), f"replay {step} differs from the eager call"
+        _check_extend(eng, layer, fb, q_static, got, fb.before, [n] * bs, f"draft extend replay {step}")
 
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float8_e5m2])
