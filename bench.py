@@ -240,14 +240,53 @@ def _cpu_baseline(w, budget_s):
         if n >= B or t >= budget_s / 4:
             break
         n = min(B, max(n + 1, int(n * min(8.0, max(2.0, (budget_s / 4) / max(t, 1e-3))))))
-    reps = max(1, min(3, int(budget_s / max(t, 1e-3)) - 1))
+    # a whole batch that takes well under the budget (the single-sequence decode) is run
+    # `inner` times per timed pass, so a pass is long enough for the clock to resolve
+    inner = max(1, int((budget_s / 8) / max(t, 1e-6))) if t < budget_s / 8 else 1
+    reps = max(1, min(3, int(budget_s / max(t * inner, 1e-3)) - 1))
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        run(rows)
-        times.append(time.perf_counter() - t0)
+        for _ in range(inner):
+            run(rows)
+        times.append((time.perf_counter() - t0) / inner)
     del kc, vc, qc
-    return statistics.median(times), rows, cores
+    return statistics.median(times), rows, cores, inner
+
+
+def _graph_us_per_call(index, calls=20, replays=20):
+    """Microseconds per call of workload ``index`` replayed from a captured HIP graph of
+    ``calls`` back-to-back calls (as an engine's decode graph runner replays them), HIP
+    events around ``replays`` replays: the GPU-side latency without the host's launch cost."""
+    import torch
+
+    from sglang_restomod_amd import workloads
+
+    w = workloads.make(index, device=torch.device("cuda:0"))
+    fn = _runner(w)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(replays):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / (replays * calls)
+    del graph, w, fn
+    torch.cuda.empty_cache()
+    return us
 
 
 def _measure_kv_write(steps, warmup):
@@ -311,6 +350,10 @@ def _measure(index, steps, warmup, cpu_seconds, kv_format="e4m3"):
     }
     res["hbm_frac"] = res["GBps"] / HBM_PEAK_GBS
     res["mfma_frac"] = res["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
+    if w.mode == "decode":
+        from sglang_restomod_amd.attention.mi355x import ops
+
+        res["kernel"] = ops.decode_kernel(w.batch, w.heads, w.heads_kv, w.dim, max(w.seq_lens_cpu))
     if w.mode != "extend":
         # the same number of K and V rows, gathered from random slots with no arithmetic
         row_bytes = w.dim * w.k_pool.element_size()
@@ -318,9 +361,9 @@ def _measure(index, steps, warmup, cpu_seconds, kv_format="e4m3"):
         res["gather_ceiling_GBps"] = _gather_ceiling(tokens, w.heads_kv, row_bytes)
         res["gather_row_bytes"] = row_bytes
     if cpu_seconds:
-        sec, rows, cores = _cpu_baseline(w, cpu_seconds)
+        sec, rows, cores, inner = _cpu_baseline(w, cpu_seconds)
         sb, sf = workloads.algorithmic_bytes(w, rows), workloads.algorithmic_flops(w, rows)
-        res["cpu"] = {"seconds": sec, "cores": cores, "sequences": len(rows), "of": w.batch,
+        res["cpu"] = {"seconds": sec, "cores": cores, "sequences": len(rows), "of": w.batch, "inner": inner,
                       "GBps": sb / sec / 1e9, "TFLOPs": sf / sec / 1e12,
                       "tokens_per_s": sum(w.extend_lens.tolist()[b] for b in rows) / sec}
     del w, fn
@@ -330,15 +373,24 @@ def _measure(index, steps, warmup, cpu_seconds, kv_format="e4m3"):
 
 def _cpu_obj(r, bound_hbm):
     c = r["cpu"]
+    rep = f" (each pass the mean of {c['inner']} back-to-back calls)" if c["inner"] > 1 else ""
     return {
         "value": round(c["GBps"] if bound_hbm else c["TFLOPs"], 5),
         "unit": "GB/s" if bound_hbm else "TFLOP/s",
         "cores": c["cores"],
         "kind": "port",
+        "seconds_per_call": round(c["seconds"], 6),
         "sample": (f"torch-native SDPA restatement (per-sequence gather + fp32 SDPA) over the {c['sequences']} "
-                   f"shortest of {c['of']} sequences, median of up to 3 passes of {c['seconds']:.3f} s; value = "
+                   f"shortest of {c['of']} sequences, median of up to 3 passes of {c['seconds']:.4g} s{rep}; value = "
                    f"algorithmic {'bytes' if bound_hbm else 'flops'} of those sequences per second"),
     }
+
+
+def _decode_kernel(r):
+    """The kernel that carries a decode or verify call: the split-KV partial, or the
+    any-head-dim kernel for head dims the tuned kernels do not take and for decode batches
+    small enough to run as one launch (ops.decode_path)."""
+    return r.get("kernel") or "splitkv_partial"
 
 
 def _roofline(r, kernel, bound_hbm):
@@ -353,7 +405,9 @@ def _roofline(r, kernel, bound_hbm):
         "traffic": _traffic(kernel, r["profile_name"]),
         "kernel_ms": round(r["event_ms_mean"], 5),
         "timing": "HIP events on the launch stream around each call ("
-                  + ("any-head-dim kernel" + ("" if bound_hbm else ", after the work-list plan") if kernel == "any_kernel"
+                  + (("any-head-dim kernel over key pieces + merge" if r["mode"] == "decode" else "any-head-dim kernel")
+                     if kernel == "any_kernel" and bound_hbm
+                     else "any-head-dim kernel, after the work-list plan" if kernel == "any_kernel"
                      else "split-KV partial + merge" if bound_hbm else "plan + extend kernel") + ")",
     }
     if bound_hbm:
@@ -430,15 +484,19 @@ def main():
             line["extend"] = _family(_measure(2, steps, args.warmup, sec_cpu), "extend_kernel", False)
         fp8 = {}
         for fmt in ("e4m3", "e5m2"):
-            fp8[fmt] = _family(_measure(3, steps, args.warmup, sec_cpu if fmt == "e4m3" else 0, kv_format=fmt),
-                               "splitkv_partial", True)
+            fp8[fmt] = _family(_measure(3, steps, args.warmup, sec_cpu, kv_format=fmt), "splitkv_partial", True)
         line["fp8_decode"] = fp8
         if args.workload != 4:
             line["verify"] = _family(_measure(4, steps, args.warmup, sec_cpu), "splitkv_partial", True)
         if args.workload != 0:
-            r = _measure(0, steps, args.warmup, 0)
-            line["decode_b1"] = {"workload": r["workload"], "us_per_call": round(r["event_ms_mean"] * 1e3, 2),
-                                 "wall_us_per_call": round(r["ms_per_step"] * 1e3, 2)}
+            # the single-sequence decode: latency-bound, so its call time in microseconds too
+            r = _measure(0, max(steps, 50), args.warmup, sec_cpu)
+            obj = _family(r, _decode_kernel(r), True)
+            obj["us_per_call"] = round(r["event_ms_mean"] * 1e3, 2)
+            obj["wall_us_per_call"] = round(r["ms_per_step"] * 1e3, 2)
+            # the same call replayed from a HIP graph: no host launch cost between its kernels
+            obj["graph_us_per_call"] = round(_graph_us_per_call(0), 2)
+            line["decode_b1"] = obj
         line["kv_write"] = _measure_kv_write(steps, args.warmup)
         # the other head dims of the reference's tuned configurations: 256 on the split-KV and
         # tiled extend kernels, 512 on the any-head-dim kernel
