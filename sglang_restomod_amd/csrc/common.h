@@ -99,12 +99,15 @@ __device__ __forceinline__ f32x4 mfma16t(const u32x4& a, const u32x4& b, f32x4 c
 // the sums are fp32, so the result is the same up to rounding; O is rescaled rarely.
 constexpr float kLazyRescale = 8.f;
 
-// Max of three floats as one v_max3_f32. Scores come straight from MFMAs, which the
-// compiler would quiet first (one more v_max per value) before fmaxf; scores hold no NaN.
+// Max of three floats; the compiler makes it one v_max3_f32 (also straight from MFMA
+// results, with no quieting v_max first). It must stay compiler code, not inline
+// assembly: the hardware does not interlock a VALU read of an MFMA result, and the
+// compiler inserts the wait states that read needs only for instructions it knows. An
+// inline-assembly v_max3 placed right after the score MFMAs read partly accumulated
+// scores (a row max from a stale accumulator, seen as run-to-run differences of the
+// fp16 extend at head dim 256).
 __device__ __forceinline__ float max3f(float x, float y, float z) {
-  float r;
-  __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
-  return r;
+  return __builtin_fmaxf(__builtin_fmaxf(x, y), z);
 }
 
 // Maximum of N scores by three-input maxima.

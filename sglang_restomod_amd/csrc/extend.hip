@@ -93,6 +93,8 @@ struct ExtendArgs {
   void* out;
   int64_t out_stride_tok, out_stride_head;  // elements of the output dtype
   int out_f32;                              // out holds fp32 (else the query dtype)
+  int head_dim;                             // the rows' head dim (<= the kernel's D when padded)
+  int chunks;                               // 16-byte chunks of one K/V row at head_dim
 };
 
 // Keys [lo, hi) that some row of the bm-row tile starting at row r0 of a sequence may see.
@@ -242,7 +244,11 @@ __global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const Exte
   for (int i = m + tid; i < a.capacity; i += kPlanThreads) items[i] = row_tile_item(-1, -1);
 }
 
-template <int D, bool QBF16, int KV>
+// PAD: the rows' head dim is below D (a multiple of 16 that has no kernel of its own):
+// every load stays in its row, the chunks past head_dim reading the row's last chunk
+// again; those K dims meet Q dims that are zero, and the output dims they feed are not
+// stored.
+template <int D, bool QBF16, int KV, bool PAD>
 __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArgs args) {
   const ExtendArgs a = args;  // local copy: the lambdas capture by reference
   constexpr int kXD = D;
@@ -321,8 +327,10 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     const uint16_t MA_GLOBAL* qp =
         qbase + (int64_t)(tok0 + t) * a.q_stride_tok + (int64_t)(h * a.group + g) * a.q_stride_head + j * (kXD / 4);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qv[rb][kk] = real[rb] ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + kk * 8) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < KK; ++kk) {
+      const bool in_dim = !PAD || j * (kXD / 4) + kk * 8 < a.head_dim;
+      qv[rb][kk] = (real[rb] && in_dim) ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + kk * 8) : u32x4{0, 0, 0, 0};
+    }
   }
   // Q is waited for here, once. The compiler cannot count the loads issued by inline
   // assembly below, so a Q load still outstanding at the first score MFMA in the loop
@@ -366,6 +374,11 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     if constexpr (kFp8) return kCPR >= 8 ? ((t & 3) | ((t >> 2) & 4)) : (t & (kCPR - 1));
     else return (2 * t) & (kCPR - 2);
   };
+  // the row's 16-byte chunk a DMA lane reads: chunk c, or the row's last one past head_dim
+  auto src_chunk = [&](int c) __attribute__((always_inline)) -> int {
+    if constexpr (PAD) return min(c, a.chunks - 1);
+    else return c;
+  };
 
   // ---- memory pipeline ----
   // Lane l looks up the slot of key l of a tile; tiles past the last are clamped to it
@@ -402,7 +415,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       const int sl = shfl_i(myslot, is_k ? xb * 16 + c : tok);
       const unsigned char MA_GLOBAL* row = (is_k ? kbase : vbase) + (uint64_t)(uint32_t)sl * row_bytes32 + head_off;
       // K: lane l -> key 16 * xb + (l & 15), 16-byte chunk kKSub * j (kKSub = 1)
-      const int chunk = is_k ? kKSub * j : (pos ^ swz(tok));
+      const int chunk = src_chunk(is_k ? kKSub * j : (pos ^ swz(tok)));
       dma(row + chunk * 16, (is_k ? kl : vl) + xb * 1024);
     } else {
       // all slot shuffles first, so that their LDS round trips overlap; this wave's K blocks
@@ -420,7 +433,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
 #pragma unroll
       for (int x = 0; x < kKBlk; ++x) {
         const int blk = wave * kKBlk + x;
-        dma(kp + (kKSub * j + blk % kKSub) * 16, kl + blk * 1024);
+        dma(kp + src_chunk(kKSub * j + blk % kKSub) * 16, kl + blk * 1024);
       }
       // V: rows of this wave's blocks, row-major, 16-byte chunks XOR-swizzled by row
 #pragma unroll
@@ -428,7 +441,8 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
         const int xb = wave * kVBlk + x;
         const int tok = (64 / kCPR) * xb + lane / kCPR;
         const int pos = lane % kCPR;
-        dma(vbase + (uint64_t)(uint32_t)vslot[x] * row_bytes32 + head_off + ((pos ^ swz(tok)) << 4), vl + xb * 1024);
+        dma(vbase + (uint64_t)(uint32_t)vslot[x] * row_bytes32 + head_off + (src_chunk(pos ^ swz(tok)) << 4),
+            vl + xb * 1024);
       }
     }
   };
@@ -644,24 +658,28 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     const float inv = (lt > 0.f) ? a.v_scale / lt : 0.f;
     const int64_t off = (int64_t)(tok0 + t) * a.out_stride_tok + (int64_t)(h * a.group + g) * a.out_stride_head;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) store_out4<QBF16>(a.out, off + db * 16 + 4 * j, o[rb][db], inv, a.out_f32);
+    for (int db = 0; db < DB; ++db)
+      if (!PAD || db * 16 + 4 * j < a.head_dim)
+        store_out4<QBF16>(a.out, off + db * 16 + 4 * j, o[rb][db], inv, a.out_f32);
   }
 }
 
-template <int D, bool QBF16>
+template <int D, bool QBF16, bool PAD>
 static hipError_t launch_extend_q(int kv, dim3 grid, hipStream_t st, const ExtendArgs& a) {
   if (kv == DT_E4M3)
-    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E4M3>), grid, dim3(kXWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E4M3, PAD>), grid, dim3(kXWaves * 64), 0, st, a);
   else if (kv == DT_E5M2)
-    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E5M2>), grid, dim3(kXWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E5M2, PAD>), grid, dim3(kXWaves * 64), 0, st, a);
   else
-    hipLaunchKernelGGL((extend_kernel<D, QBF16, QBF16 ? DT_BF16 : DT_F16>), grid, dim3(kXWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, QBF16 ? DT_BF16 : DT_F16, PAD>), grid, dim3(kXWaves * 64), 0, st, a);
   return hipGetLastError();
 }
 
 template <int D>
 static hipError_t launch_extend_d(bool qbf16, int kv, dim3 grid, hipStream_t st, const ExtendArgs& a) {
-  return qbf16 ? launch_extend_q<D, true>(kv, grid, st, a) : launch_extend_q<D, false>(kv, grid, st, a);
+  const bool pad = a.head_dim != D;
+  if (pad) return qbf16 ? launch_extend_q<D, true, true>(kv, grid, st, a) : launch_extend_q<D, false, true>(kv, grid, st, a);
+  return qbf16 ? launch_extend_q<D, true, false>(kv, grid, st, a) : launch_extend_q<D, false, false>(kv, grid, st, a);
 }
 
 }  // namespace ma
@@ -673,9 +691,18 @@ static int64_t extend_items(int64_t num_tokens, int group, int batch, int bm) {
   return (num_tokens * group + bm - 1) / bm + batch;
 }
 
+// The tiled extend kernel that serves a head dim: 64, 128 or 256, padded up from the
+// multiples of 16 below (their MFMA work is that of the padded dim), or 0 above 256 (the
+// any-head-dim kernel).
+static int extend_kernel_dim(int head_dim) {
+  if (head_dim < 16 || head_dim % 16) return 0;
+  return head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : head_dim <= 256 ? 256 : 0;
+}
+
 // Rows per workgroup of the extend kernel at a head dim (0 if unsupported).
 static int extend_tile_rows(int head_dim) {
-  return head_dim == 64 ? XShape<64>::BM : head_dim == 128 ? XShape<128>::BM : head_dim == 256 ? XShape<256>::BM : 0;
+  const int d = extend_kernel_dim(head_dim);
+  return d == 64 ? XShape<64>::BM : d == 128 ? XShape<128>::BM : d == 256 ? XShape<256>::BM : 0;
 }
 
 extern "C" size_t ma_extend_workspace_bytes(int64_t num_tokens, int num_q_heads, int num_kv_heads, int batch) {
@@ -694,7 +721,10 @@ extern "C" int ma_paged_extend(
     int causal, int sliding_window, float softmax_scale, float k_scale, float v_scale,
     void* workspace, size_t workspace_bytes, void* out, int out_dtype, int64_t out_stride_tok,
     int64_t out_stride_head, void* stream) {
-  const bool generic = any_head_dim(head_dim);  // served by the any-head-dim kernel
+  // head dims up to 256 run on the tiled kernels (padded up to 64, 128 or 256), the
+  // wider ones on the any-head-dim kernel
+  const int kdim = extend_kernel_dim(head_dim);
+  const bool generic = kdim == 0 && any_head_dim(head_dim);
   const int bm = generic ? kAnyPlanRows : extend_tile_rows(head_dim);
   if (bm == 0) return set_error(MA_EUNSUPPORTED, "head_dim %d not supported (multiples of 16 up to %d)", head_dim, kAnyMaxDim);
   if (q_dtype != DT_F16 && q_dtype != DT_BF16) return set_error(MA_EINVAL, "q dtype %d must be f16 or bf16", q_dtype);
@@ -734,7 +764,7 @@ extern "C" int ma_paged_extend(
   p.num_tokens = (int)num_tokens;
   p.batch = batch; p.group = group; p.causal = causal ? 1 : 0; p.window = sliding_window < 0 ? -1 : sliding_window;
   p.tile_rows = bm;
-  p.tile_keys = generic ? kAnyKeys : head_dim == 256 ? XShape<256>::BN : XShape<128>::BN;
+  p.tile_keys = generic ? kAnyKeys : kdim == 256 ? XShape<256>::BN : XShape<128>::BN;
   p.capacity = (int)items; p.items = reinterpret_cast<int64_t*>(workspace);
   hipLaunchKernelGGL(extend_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
@@ -769,9 +799,11 @@ extern "C" int ma_paged_extend(
   a.out_f32 = out_dtype == DT_F32;
   const dim3 grid((unsigned)(items * num_kv_heads));
   const bool qbf16 = q_dtype == DT_BF16;
-  e = head_dim == 64    ? launch_extend_d<64>(qbf16, kv_dtype, grid, (hipStream_t)stream, a)
-      : head_dim == 128 ? launch_extend_d<128>(qbf16, kv_dtype, grid, (hipStream_t)stream, a)
-                        : launch_extend_d<256>(qbf16, kv_dtype, grid, (hipStream_t)stream, a);
+  a.head_dim = head_dim;
+  a.chunks = head_dim * elt / 16;  // >= 1: head_dim is a multiple of 16
+  e = kdim == 64    ? launch_extend_d<64>(qbf16, kv_dtype, grid, (hipStream_t)stream, a)
+      : kdim == 128 ? launch_extend_d<128>(qbf16, kv_dtype, grid, (hipStream_t)stream, a)
+                    : launch_extend_d<256>(qbf16, kv_dtype, grid, (hipStream_t)stream, a);
   if (e != hipSuccess) return set_error(MA_ELAUNCH, "extend launch failed: %s", hipGetErrorString(e));
   return MA_OK;
 }

@@ -844,7 +844,12 @@ static hipError_t launch_any_m(int kv, dim3 grid, hipStream_t st, const AnyArgs&
 
 template <int DP, bool QBF16>
 static hipError_t launch_any_q(int kv, dim3 grid, hipStream_t st, const AnyArgs& a) {
-  return a.items ? launch_any_m<DP, QBF16, true>(kv, grid, st, a) : launch_any_m<DP, QBF16, false>(kv, grid, st, a);
+  // extend rows reach this kernel above 256 dims only (the tiled extend kernels take the rest)
+  if (a.items) {
+    if constexpr (DP == 512) return launch_any_m<DP, QBF16, true>(kv, grid, st, a);
+    else return hipErrorInvalidValue;
+  }
+  return launch_any_m<DP, QBF16, false>(kv, grid, st, a);
 }
 
 template <int DP>

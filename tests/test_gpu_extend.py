@@ -356,3 +356,31 @@ def test_bf16_v_outside_fp16_range():
     err_dec = float(np.abs(dec.double().cpu().numpy() - ref_dec).max())
     print(f"[result] decode: max |err| vs exact V {err_dec:.3e}", flush=True)
     assert err_dec <= 2e-3 * vmax, err_dec
+
+
+@pytest.mark.parametrize("index,dtype", [(6, torch.float16), (6, torch.bfloat16), (2, torch.float16),
+                                         (10, torch.float16), (9, torch.bfloat16)])
+def test_extend_is_deterministic(index, dtype):
+    """Repeated calls on the same inputs give the same bits, fp32 output included: the
+    extend batch at head dims 256 (fp16 and bf16), 128, and 192 and 96 (padded onto the
+    256 and 128 kernels). A VALU read of an MFMA result before the result is written
+    (a hazard the hardware does not interlock) shows up here as run-to-run differences."""
+    from sglang_restomod_amd.attention.mi355x import ops
+
+    dev = torch.device("cuda:0")
+    w = workloads.make(index, device=dev, batch=4, scale_lens=0.5)
+    w.q, w.k_pool, w.v_pool = w.q.to(dtype), w.k_pool.to(dtype), w.v_pool.to(dtype)
+    print(f"[case] extend determinism {w.name} {dtype}", flush=True)
+
+    def run(out_dtype):
+        out = torch.empty(w.q.shape, dtype=out_dtype, device=dev)
+        ops.paged_extend_forward(w.q, w.k_pool, w.v_pool, w.req_to_token, w.seq_lens, w.query_start_loc,
+                                 w.prefix_lens, softmax_scale=w.softmax_scale, out=out,
+                                 row_index=w.req_pool_indices)
+        torch.cuda.synchronize()
+        return out
+
+    for out_dtype in (dtype, torch.float32):
+        first = run(out_dtype)
+        for _ in range(4):
+            assert torch.equal(run(out_dtype), first), f"{w.name} {dtype} -> {out_dtype}: run-to-run difference"
