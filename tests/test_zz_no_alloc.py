@@ -2,11 +2,17 @@
 bit-identical outputs on two calls in a row, the second on a smaller batch (the static
 scratch keeps the first call's contents), at head dims 128, 256 and 512 (the last on the
 any-head-dim kernel, which uses no scratch) and with fp8 KV; a grid beyond the scratch is
-refused before any launch."""
+refused before any launch. In a fresh process, the first call (which looks up the scratch's
+address on the device) can be made inside HIP graph capture, and a warm call leaves the
+device's free memory unchanged."""
 
 from __future__ import annotations
 
 import ctypes
+import os
+import subprocess
+import sys
+import textwrap
 
 import pytest
 import torch
@@ -72,3 +78,47 @@ def test_noalloc_refuses_a_grid_beyond_its_scratch():
     assert rc == _lib.MA_EINVAL
     assert b"static scratch" in lib.ma_last_error()
     del keep
+
+
+_FIRST_CALL_IN_CAPTURE = textwrap.dedent("""
+    import ctypes, sys, torch
+    sys.path.insert(0, {root!r})
+    from sglang_restomod_amd import workloads
+    from sglang_restomod_amd.attention.mi355x import _lib, ops
+    from tests.test_zz_no_alloc import _args
+    dev = torch.device("cuda:0")
+    lib = _lib.load()
+    nwg = min(ops.splitkv_workgroups(dev), _lib.MA_NOALLOC_MAX_WORKGROUPS)
+    w = workloads.make(1, device=dev, batch=6, scale_lens=0.2)
+    got = torch.full_like(w.q, float("nan"))
+    head, tail, keep = _args(w, got, nwg)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):   # the process's first noalloc call: scratch lookup inside capture
+        rc = lib.ma_grouped_decode_noalloc(*head, *tail)
+    assert rc == 0, lib.ma_last_error()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    want = torch.empty_like(w.q)
+    h2, t2, keep2 = _args(w, want, nwg)
+    ws = ops.splitkv_workspace(dev, num_workgroups=nwg, head_dim=w.dim)
+    assert lib.ma_grouped_decode(*h2, ws.data_ptr(), ws.numel(), *t2) == 0, lib.ma_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), "graph replay differs from the workspace entry point"
+    # a warm call allocates nothing: the device's free memory is unchanged
+    free0 = torch.cuda.mem_get_info(dev)[0]
+    assert lib.ma_grouped_decode_noalloc(*head, *tail) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(dev)[0] == free0, "a noalloc call changed the free device memory"
+    print("FIRST_CALL_IN_CAPTURE_OK", flush=True)
+""")
+
+
+def test_noalloc_first_call_inside_graph_capture_in_a_fresh_process():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("[case] noalloc first call inside capture (subprocess)", flush=True)
+    proc = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE.format(root=root)], cwd=root,
+                          capture_output=True, text=True, timeout=180)
+    assert proc.returncode == 0 and "FIRST_CALL_IN_CAPTURE_OK" in proc.stdout, (proc.stdout[-2000:],
+                                                                                proc.stderr[-3000:])
