@@ -34,6 +34,7 @@ struct KvWriteArgs {
   int64_t cache_stride_row, cache_stride_head;  // elements of the cache dtype (bytes for fp8)
   int64_t num_slots;
   float k_div, v_div;  // divisors (1 when no scale is applied)
+  float k_rcp, v_rcp;  // their reciprocals, rounded to fp32
   int apply_scale;
 };
 
@@ -64,9 +65,34 @@ __device__ __forceinline__ uint32_t store16(float x) {
   else return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+// x / div in fp32, then rounded to the source dtype, exactly as the IEEE division and the
+// cast give it. q = x * rcp (rcp = 1 / div rounded to fp32) is within 3 fp32 ulps of the
+// IEEE quotient (two roundings of relative size 2^-24 each, against the quotient's own
+// half ulp), so both round to the same 16-bit value unless a 16-bit rounding boundary
+// lies within 3 ulps of q; then (rarely) the division is done. The boundaries: bf16 rounds
+// at the low 16 bits of the fp32 pattern (boundary 0x8000), fp16 at the low 13 bits
+// (0x1000) in its normal range; below fp16's smallest normal the division is always done.
+template <int SRC>
+__device__ __forceinline__ float div_to_src(float x, float div, float rcp) {
+  const float q = x * rcp;
+  const uint32_t b = __builtin_bit_cast(uint32_t, q);
+  bool near;
+  if constexpr (SRC == DT_BF16) {
+    const int low = (int)(b & 0xffffu) - 0x8000;
+    near = low >= -3 && low <= 3;
+  } else {
+    const int low = (int)(b & 0x1fffu) - 0x1000;
+    near = (low >= -3 && low <= 3) || (b & 0x7f800000u) < (113u << 23);
+  }
+  float exact = q;
+  if (__builtin_expect(near, 0)) exact = x / div;  // lanes near a boundary only
+  return h2f<SRC == DT_BF16>(store16<SRC>(exact));
+}
+
 // One 16-byte chunk of 8 source values -> cache values.
 template <int SRC, int DST>
-__device__ __forceinline__ void convert_chunk(const u32x4 in, float div, bool apply, u32x4& out16, u32x2& out8) {
+__device__ __forceinline__ void convert_chunk(const u32x4 in, float div, float rcp, bool apply, u32x4& out16,
+                                              u32x2& out8) {
   if constexpr (SRC == DST) {
     out16 = in;  // same dtype: a copy (no scale is applied, as in the pool)
     return;
@@ -77,7 +103,7 @@ __device__ __forceinline__ void convert_chunk(const u32x4 in, float div, bool ap
   if (apply) {
     // divide in fp32 and round to the source dtype, as the source-dtype division does
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = h2f<SRC == DT_BF16>(store16<SRC>(x[i] / div));
+    for (int i = 0; i < 8; ++i) x[i] = div_to_src<SRC>(x[i], div, rcp);
   }
   if constexpr (DST == DT_E4M3 || DST == DT_E5M2) {
 #pragma unroll
@@ -118,7 +144,7 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const KvWriteArgs args) {
   const u32x4 in = *reinterpret_cast<const u32x4 MA_GLOBAL*>(src);
   u32x4 o16;
   u32x2 o8;
-  convert_chunk<SRC, DST>(in, which ? a.v_div : a.k_div, a.apply_scale != 0, o16, o8);
+  convert_chunk<SRC, DST>(in, which ? a.v_div : a.k_div, which ? a.v_rcp : a.k_rcp, a.apply_scale != 0, o16, o8);
   const int64_t off = slot * a.cache_stride_row + (int64_t)h * a.cache_stride_head + part * 8;
   if constexpr (kFp8) {
     unsigned char MA_GLOBAL* dst = gptr_mut(reinterpret_cast<unsigned char*>(which ? a.v_cache : a.k_cache)) + off;
@@ -175,6 +201,8 @@ extern "C" int ma_set_kv_buffer(const void* k, const void* v, int64_t src_stride
   a.apply_scale = apply_scale ? 1 : 0;
   a.k_div = apply_scale ? k_scale : 1.f;
   a.v_div = apply_scale ? v_scale : 1.f;
+  a.k_rcp = 1.f / a.k_div;  // IEEE fp32 on the host
+  a.v_rcp = 1.f / a.v_div;
   const int64_t per_block = 256 / a.chunks;  // tokens per block (head_dim <= 2048: at least 1)
   a.per_block = (int)per_block;
   a.chunk_shift = (a.chunks & (a.chunks - 1)) ? -1 : __builtin_ctz((unsigned)a.chunks);
