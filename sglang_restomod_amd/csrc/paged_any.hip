@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
   };
   const unsigned char MA_GLOBAL* kbase = gptr(reinterpret_cast<const unsigned char*>(a.k));
   const unsigned char MA_GLOBAL* vbase = gptr(reinterpret_cast<const unsigned char*>(a.v));
-  const int64_t row_bytes = a.kv_stride_row * kElt;
+  const uint32_t row_bytes32 = (uint32_t)(a.kv_stride_row * kElt);  // the hosts check it fits
   const int page_mask = (1 << a.tt.page_shift) - 1;
 
   // One wave's 16 rows r0 .. r0 + 15 of sequence b, kv head h. Shared mode: the
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
     };
     auto load_k = [&](int myslot, u32x4 (&kr)[kKL]) __attribute__((always_inline)) {
       const int kslot = shfl_i(myslot, c);
-      const unsigned char MA_GLOBAL* krow = kbase + (int64_t)kslot * row_bytes + head_off;
+      const unsigned char MA_GLOBAL* krow = kbase + (uint64_t)(uint32_t)kslot * row_bytes32 + head_off;
 #pragma unroll
       for (int x = 0; x < kKL; ++x) {
         const int d0 = min(kFp8 ? x * 64 + j * 16 : x * 32 + j * 8, D - (kFp8 ? 16 : 8));
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
         const int tr = u / kUnits;
         const int q = min(u - tr * kUnits, D / 8 - 1);
         const int vs = shfl_i(myslot, tr);
-        vr[x] = *reinterpret_cast<const VRaw MA_GLOBAL*>(vbase + (int64_t)vs * row_bytes + head_off + q * 8 * kElt);
+        vr[x] = *reinterpret_cast<const VRaw MA_GLOBAL*>(vbase + (uint64_t)(uint32_t)vs * row_bytes32 + head_off + q * 8 * kElt);
       }
     };
     // V units -> fp16 -> this wave's LDS block, row-major with padded rows (the transposed
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(kAnyWaves * 64, (any_wg_per_cu<SHARED, DP>())) void
           const int u = min((int)threadIdx.x + kAnyWaves * 64 * x, kTileUnits - 1);
           const int key = u / kUnits;
           const int q = min(u - key * kUnits, D / 8 - 1);
-          const int64_t off = (int64_t)shfl_i(myslot, key) * row_bytes + head_off + q * 8 * kElt;
+          const int64_t off = (int64_t)((uint64_t)(uint32_t)shfl_i(myslot, key) * row_bytes32) + head_off + q * 8 * kElt;
           if constexpr (kFp8) {
             const u32x2 w = *reinterpret_cast<const u32x2 MA_GLOBAL*>(kbase + off);
             kraw[x] = u32x4{w[0], w[1], 0u, 0u};

@@ -93,6 +93,7 @@ struct SplitKVArgs {
   float scale_log2;          // softmax_scale * k_scale * log2(e)
   float v_scale;
   int nwaves;                // waves of the persistent grid
+  int merge_split;           // merge workgroups per wave: 1, or one per row set of a row group
   int* desc;                 // [nwaves][kDescInts] shared segment ending in each wave's first piece
   float* part_o;             // [nwaves][2][kMaxRows][D]
   float* part_lse;           // [nwaves][2][kMaxRows]
@@ -367,7 +368,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
 
   const unsigned char MA_GLOBAL* kbase = gptr(reinterpret_cast<const unsigned char*>(a.k));
   const unsigned char MA_GLOBAL* vbase = gptr(reinterpret_cast<const unsigned char*>(a.v));
-  const int64_t row_bytes = a.kv_stride_row * kElt;
+  const uint32_t row_bytes32 = (uint32_t)(a.kv_stride_row * kElt);  // the host checks it fits
   const int64_t head_bytes = a.kv_stride_head * kElt;
 
   // XOR swizzle of the 16-byte chunks of V row t in LDS (spreads the transposed reads
@@ -419,15 +420,23 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   // into registers. Loads complete in issue order, so once the compiler has waited for
   // this tile's K registers, its V rows are in LDS as well.
   auto issue = [&](const Cursor& cu, int myslot, Raw& r, int stage) __attribute__((always_inline)) {
-    const int64_t hoff = (int64_t)cu.h * head_bytes;
+    const uint64_t hoff = (uint64_t)cu.h * (uint64_t)head_bytes;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)vring[wave][stage];
+    // Byte offset of the row that load x of this lane reads (its slot times the row
+    // stride, plus the head): K and V read the same rows, so one lookup and one 32 x 32
+    // -> 64-bit multiply serve both (the host keeps the row stride below 4 GiB).
+    uint64_t roff[kVL];
+#pragma unroll
+    for (int x = 0; x < kVL; ++x) {
+      const int tok = (64 / kCPR) * x + lane / kCPR;
+      roff[x] = (uint64_t)(uint32_t)shfl_i(myslot, tok) * row_bytes32 + hoff;
+    }
 #pragma unroll
     for (int x = 0; x < kVL; ++x) {
       // one instruction: 64 / kCPR whole rows, lane -> (row, 16-byte chunk)
       const int tok = (64 / kCPR) * x + lane / kCPR;
       const int pos = lane % kCPR;
-      const int slot = shfl_i(myslot, tok);
-      const unsigned char MA_GLOBAL* src = vbase + (int64_t)slot * row_bytes + hoff + ((pos ^ swz(tok)) << 4);
+      const unsigned char MA_GLOBAL* src = vbase + roff[x] + ((pos ^ swz(tok)) << 4);
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + x * 1024);
       __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" MA_V_POLICY : : "s"(m0), "v"(src) : "memory", "m0");
     }
@@ -437,8 +446,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     for (int x = 0; x < kVL; ++x) {
       const int tok = (64 / kCPR) * x + lane / kCPR;
       const int pos = lane % kCPR;
-      const int slot = shfl_i(myslot, tok);
-      const unsigned char MA_GLOBAL* kp = kbase + (int64_t)slot * row_bytes + hoff + ((pos ^ swzk(tok)) << 4);
+      const unsigned char MA_GLOBAL* kp = kbase + roff[x] + ((pos ^ swzk(tok)) << 4);
       __asm__ volatile("global_load_dwordx4 %0, %1, off" MA_K_POLICY : "=a"(r.k[x]) : "v"(kp) : "memory");
     }
   };
@@ -812,19 +820,26 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
 // successive pieces do not wait for each other's math. 256 threads cover 1024 / D rows x
 // D head-dim entries per pass.
 // ---------------------------------------------------------------------------
-// Merge workgroups per partial-kernel wave: one per 8-row set of a 32-row group.
+// Row sets (1024 / D rows: one pass of a 256-thread merge workgroup) of a row group.
 template <int D, int NB>
-constexpr int merge_split() {
-  return NB == 1 ? 1 : (16 * NB) / (1024 / D);
+constexpr int merge_passes() {
+  return (16 * NB) / (1024 / D) > 0 ? (16 * NB) / (1024 / D) : 1;
+}
+// Merge workgroups per partial-kernel wave: one per row set when more than one row set
+// holds real rows (they then merge in parallel), else one for the whole row group.
+template <int D, int NB>
+static int merge_split(int rows_total) {
+  const int real_rows = rows_total < 16 * NB ? rows_total : 16 * NB;
+  return real_rows > 1024 / D ? merge_passes<D, NB>() : 1;
 }
 
 template <int D, int NB, bool QBF16>
 __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
   const SplitKVArgs a = args;
   constexpr int kRows = 16 * NB;
-  constexpr int kSplit = merge_split<D, NB>();  // workgroups per partial-kernel wave
-  const int W = blockIdx.x / kSplit;
-  const int part = blockIdx.x - W * kSplit;
+  const int split = a.merge_split;  // workgroups per partial-kernel wave: 1 or kPass
+  const int W = blockIdx.x / split;
+  const int part = blockIdx.x - W * split;
   const int MA_CONST* dsc = cptr(a.desc) + (int64_t)W * kDescInts;
   if (dsc[0] == 0) return;
   const int b = dsc[1], h = dsc[2], rg = dsc[3], w1 = dsc[4], sel1 = dsc[5];
@@ -835,18 +850,16 @@ __global__ __launch_bounds__(256) void splitkv_merge(const SplitKVArgs args) {
   constexpr int kRPP = 256 / kTPR;  // rows per pass of the workgroup
   const int d4 = (threadIdx.x % kTPR) * 4;
   const int r_base = threadIdx.x / kTPR;
-  // thread: rows r_base + kRPP i, head-dim entries d4..d4+3. 16-row groups: one
-  // workgroup takes both row sets, one after the other (the second is padding when G = 8).
-  // 32-row groups: each row set has a workgroup of its own. Within a row set the pieces
+  // thread: rows r_base + kRPP i, head-dim entries d4..d4+3. Each row set has a workgroup
+  // of its own (one whose rows are all GQA padding returns at once). Within a row set the pieces
   // are the outer loop (unrolled by four), so the loads of four pieces are in flight
   // together. Measured at D=128 on a verify batch of 32 x 4 tokens: 13 us with one row
   // set at a time in one workgroup, 10 us with all four together, 8.0 us with a
   // workgroup per row set; about 5 us on a decode batch of 64.
-  constexpr int kPass = kRows / kRPP > 0 ? kRows / kRPP : 1;
+  constexpr int kPass = merge_passes<D, NB>();
+  static_assert(kPass == (kRows / kRPP > 0 ? kRows / kRPP : 1), "a row set is one pass");
   constexpr int kChunk = 1;
-  static_assert(kSplit == 1 || kSplit == kPass, "a split workgroup takes one row set");
-#pragma unroll
-  for (int c0 = kSplit == 1 ? 0 : part; c0 < (kSplit == 1 ? kPass : part + 1); c0 += kChunk) {
+  for (int c0 = split == 1 ? 0 : part; c0 < (split == 1 ? kPass : part + 1); c0 += kChunk) {
     bool live = false;  // rows past the last query token (GQA padding) are not read
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
@@ -923,7 +936,7 @@ static hipError_t launch_partial_d(int nb, bool qbf16, int kv, dim3 grid, hipStr
 template <int D>
 static hipError_t launch_merge_d(int nb, bool qbf16, int nwaves, hipStream_t st, const SplitKVArgs& a) {
   constexpr int NB2 = kMaxNB<D>;
-  const dim3 grid((unsigned)(nwaves * (nb == 1 ? merge_split<D, 1>() : merge_split<D, NB2>())));
+  const dim3 grid((unsigned)(nwaves * a.merge_split));
   if (qbf16) {
     if (nb == 1) hipLaunchKernelGGL((splitkv_merge<D, 1, true>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((splitkv_merge<D, NB2, true>), grid, dim3(256), 0, st, a);
@@ -1055,6 +1068,8 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
       ((a.q_stride_head * 2) & 15) || ((a.out_stride_tok * out_elt) & out_align) ||
       ((a.out_stride_head * out_elt) & out_align))
     return set_error(MA_EINVAL, "strides must keep rows 16-byte aligned");
+  if (a.kv_stride_row * elt >= ((int64_t)1 << 32))
+    return set_error(MA_EUNSUPPORTED, "KV row stride of %lld bytes exceeds 4 GiB", (long long)(a.kv_stride_row * elt));
   a.group = a.hq / a.hkv;
   if ((int64_t)a.num_tokens * a.group > 0x7fffffff) return set_error(MA_EINVAL, "num_tokens x GQA group exceeds 2^31");
   if (max_seq_len < 0) return set_error(MA_EINVAL, "max_seq_len must be >= 0 (0: not known)");
@@ -1111,6 +1126,9 @@ static int splitkv_run(SplitKVArgs a, int head_dim, int q_dtype, int kv_dtype, i
   a.rows = 16 * nb;
   a.row_groups = (rows_total + a.rows - 1) / a.rows;
   a.nwaves = num_workgroups * kWaves;
+  a.merge_split = head_dim == 64    ? (nb == 1 ? merge_split<64, 1>(rows_total) : merge_split<64, 2>(rows_total))
+                  : head_dim == 128 ? (nb == 1 ? merge_split<128, 1>(rows_total) : merge_split<128, 2>(rows_total))
+                                    : merge_split<256, 1>(rows_total);
   const size_t need = ma_splitkv_workspace_bytes(num_workgroups, head_dim);
   if (!workspace || workspace_bytes < need)
     return set_error(MA_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
