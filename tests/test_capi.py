@@ -75,6 +75,7 @@ def _decode_args(**over):
     ({"odt": 2}, "out dtype"),
     ({"odt": 4, "os1": 130}, "aligned"),
     ({"msl": -1}, "max_seq_len"),
+    ({"rs": 1 << 31}, "exceeds 4 GiB"),  # bf16 rows of 4 GiB: the kernels' 32-bit row stride
 ])
 def test_bad_arguments_are_rejected_before_launch(lib, over, msg):
     status = lib.ma_grouped_decode(*_decode_args(**over))
