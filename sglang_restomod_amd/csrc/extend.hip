@@ -244,13 +244,17 @@ __global__ __launch_bounds__(kPlanThreads, 1) void extend_plan_kernel(const Exte
   for (int i = m + tid; i < a.capacity; i += kPlanThreads) items[i] = row_tile_item(-1, -1);
 }
 
-// PAD: the rows' head dim is below D (a multiple of 16 that has no kernel of its own):
-// every load stays in its row, the chunks past head_dim reading the row's last chunk
-// again; those K dims meet Q dims that are zero, and the output dims they feed are not
-// stored.
-template <int D, bool QBF16, int KV, bool PAD>
+// HD: the rows' head dim. HD == D: exact. Otherwise the head dim is below D (a multiple of
+// 16 that has no kernel of its own): every load stays in its row, the chunks past head_dim
+// reading the row's last chunk again; those K dims meet Q dims that are zero, and the
+// output dims they feed are not stored. HD == 0 takes the head dim from the arguments and
+// runs every MFMA step of D; a head dim fixed at compile time (0 < HD < D) also skips the
+// score steps and output blocks that lie wholly past it.
+template <int D, bool QBF16, int KV, int HD>
 __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArgs args) {
   const ExtendArgs a = args;  // local copy: the lambdas capture by reference
+  constexpr bool PAD = HD != D;
+  constexpr int kSkipFrom = (PAD && HD != 0) ? HD : 0;  // first dim with no work, or 0
   constexpr int kXD = D;
   constexpr bool kFp8 = (KV == DT_E4M3 || KV == DT_E5M2);
   constexpr int kXBN = XShape<D>::BN;
@@ -294,6 +298,14 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
   const int j = lane >> 4;
+  // Head-dim order of the QK contraction: MFMA step kk of lane group j holds dims
+  // qdim(kk) .. +8, the 16-byte chunk 4*kk + j of a K row (fp8: steps 2h and 2h+1 split
+  // chunk 4*h + j), so that each step covers 32 consecutive dims (fp8: a pair of steps
+  // covers 64) and steps past a padded head dim hold only zeros.
+  auto qdim = [&](int kk) -> int {
+    if constexpr (kFp8) return (kk >> 1) * 64 + j * 16 + (kk & 1) * 8;
+    else return kk * 32 + j * 8;
+  };
 
   const int item = (int)blockIdx.x / a.hkv;
   const int h = (int)blockIdx.x - item * a.hkv;
@@ -325,11 +337,11 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     lo_r[rb] = (real[rb] && a.window >= 0) ? max(0, qpos - a.window) : 0;
     hi_r[rb] = real[rb] ? (a.causal ? min(seq, qpos + 1) : seq) : 0;
     const uint16_t MA_GLOBAL* qp =
-        qbase + (int64_t)(tok0 + t) * a.q_stride_tok + (int64_t)(h * a.group + g) * a.q_stride_head + j * (kXD / 4);
+        qbase + (int64_t)(tok0 + t) * a.q_stride_tok + (int64_t)(h * a.group + g) * a.q_stride_head;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      const bool in_dim = !PAD || j * (kXD / 4) + kk * 8 < a.head_dim;
-      qv[rb][kk] = (real[rb] && in_dim) ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + kk * 8) : u32x4{0, 0, 0, 0};
+      const bool in_dim = !PAD || qdim(kk) < a.head_dim;
+      qv[rb][kk] = (real[rb] && in_dim) ? *reinterpret_cast<const u32x4 MA_GLOBAL*>(qp + qdim(kk)) : u32x4{0, 0, 0, 0};
     }
   }
   // Q is waited for here, once. The compiler cannot count the loads issued by inline
@@ -414,8 +426,8 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       const int pos = lane % kCPR;
       const int sl = shfl_i(myslot, is_k ? xb * 16 + c : tok);
       const unsigned char MA_GLOBAL* row = (is_k ? kbase : vbase) + (uint64_t)(uint32_t)sl * row_bytes32 + head_off;
-      // K: lane l -> key 16 * xb + (l & 15), 16-byte chunk kKSub * j (kKSub = 1)
-      const int chunk = src_chunk(is_k ? kKSub * j : (pos ^ swz(tok)));
+      // K: lane l -> key 16 * xb + (l & 15), 16-byte chunk j (one 64-byte block per row)
+      const int chunk = src_chunk(is_k ? j : (pos ^ swz(tok)));
       dma(row + chunk * 16, (is_k ? kl : vl) + xb * 1024);
     } else {
       // all slot shuffles first, so that their LDS round trips overlap; this wave's K blocks
@@ -428,12 +440,12 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
         const int xb = wave * kVBlk + x;
         vslot[x] = shfl_i(myslot, (64 / kCPR) * xb + lane / kCPR);
       }
-      // K: lane l -> key kb_w*16 + (l & 15), 16-byte chunk kKSub*j + sub
+      // K: lane l -> key kb_w*16 + (l & 15), 16-byte chunk 4*sub + j
       const unsigned char MA_GLOBAL* kp = kbase + (uint64_t)(uint32_t)kslot * row_bytes32 + head_off;
 #pragma unroll
       for (int x = 0; x < kKBlk; ++x) {
         const int blk = wave * kKBlk + x;
-        dma(kp + src_chunk(kKSub * j + blk % kKSub) * 16, kl + blk * 1024);
+        dma(kp + src_chunk(4 * (blk % kKSub) + j) * 16, kl + blk * 1024);
       }
       // V: rows of this wave's blocks, row-major, 16-byte chunks XOR-swizzled by row
 #pragma unroll
@@ -480,7 +492,8 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
       for (int kb = 0; kb < KB; ++kb) s[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (kFp8) {
 #pragma unroll
-      for (int hh = 0; hh < kKSub; ++hh)
+      for (int hh = 0; hh < kKSub; ++hh) {
+        if (kSkipFrom && hh * 64 >= kSkipFrom) continue;  // dims past the head dim: zeros in Q
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           const u32x4 raw = *reinterpret_cast<const u32x4*>(kt + (kb * kKSub + hh) * 1024 + lane * 16);
@@ -492,15 +505,18 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
             s[rb][kb] = mfma16t<QBF16>(k1, qv[rb][2 * hh + 1], s[rb][kb]);
           }
         }
+      }
     } else {
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
+      for (int kk = 0; kk < KK; ++kk) {
+        if (kSkipFrom && kk * 32 >= kSkipFrom) continue;  // dims past the head dim: zeros in Q
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           const u32x4 kf = *reinterpret_cast<const u32x4*>(kt + (kb * kKSub + kk) * 1024 + lane * 16);
 #pragma unroll
           for (int rb = 0; rb < kXRB; ++rb) s[rb][kb] = mfma16t<QBF16>(kf, qv[rb][kk], s[rb][kb]);
         }
+      }
     }
     mid();
     const bool full = (base >= full_lo) && (base + kXBN <= full_hi);
@@ -562,6 +578,7 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
     for (int hf = 0; hf < HF; ++hf)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
+        if (kSkipFrom && db * 16 >= kSkipFrom) continue;  // output dims past the head dim: never stored
         u32x4 va;
         if constexpr (kFp8) {
           const int e = c >> 1, cc = lane & 1;
@@ -664,22 +681,32 @@ __global__ __launch_bounds__(kXWaves * 64, 1) void extend_kernel(const ExtendArg
   }
 }
 
-template <int D, bool QBF16, bool PAD>
+template <int D, bool QBF16, int HD>
 static hipError_t launch_extend_q(int kv, dim3 grid, hipStream_t st, const ExtendArgs& a) {
   if (kv == DT_E4M3)
-    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E4M3, PAD>), grid, dim3(kXWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E4M3, HD>), grid, dim3(kXWaves * 64), 0, st, a);
   else if (kv == DT_E5M2)
-    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E5M2, PAD>), grid, dim3(kXWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, DT_E5M2, HD>), grid, dim3(kXWaves * 64), 0, st, a);
   else
-    hipLaunchKernelGGL((extend_kernel<D, QBF16, QBF16 ? DT_BF16 : DT_F16, PAD>), grid, dim3(kXWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((extend_kernel<D, QBF16, QBF16 ? DT_BF16 : DT_F16, HD>), grid, dim3(kXWaves * 64), 0, st, a);
   return hipGetLastError();
 }
 
+// Padded head dims with kernels of their own (their zero score steps and output blocks
+// skipped at compile time): 96 on the 128 kernel, 192 on the 256 kernel.
+template <int D>
+constexpr int kStaticPad = D == 128 ? 96 : D == 256 ? 192 : 0;
+
 template <int D>
 static hipError_t launch_extend_d(bool qbf16, int kv, dim3 grid, hipStream_t st, const ExtendArgs& a) {
-  const bool pad = a.head_dim != D;
-  if (pad) return qbf16 ? launch_extend_q<D, true, true>(kv, grid, st, a) : launch_extend_q<D, false, true>(kv, grid, st, a);
-  return qbf16 ? launch_extend_q<D, true, false>(kv, grid, st, a) : launch_extend_q<D, false, false>(kv, grid, st, a);
+  if (a.head_dim == D)
+    return qbf16 ? launch_extend_q<D, true, D>(kv, grid, st, a) : launch_extend_q<D, false, D>(kv, grid, st, a);
+  if constexpr (kStaticPad<D> != 0) {
+    if (a.head_dim == kStaticPad<D>)
+      return qbf16 ? launch_extend_q<D, true, kStaticPad<D>>(kv, grid, st, a)
+                   : launch_extend_q<D, false, kStaticPad<D>>(kv, grid, st, a);
+  }
+  return qbf16 ? launch_extend_q<D, true, 0>(kv, grid, st, a) : launch_extend_q<D, false, 0>(kv, grid, st, a);
 }
 
 }  // namespace ma
