@@ -17,8 +17,10 @@ extend TFLOP/s against the bf16 MFMA roofline), so one JSON line carries:
   e5m2 pools; ``verify``: workload 4 (B=32, 4 draft tokens, P U[2048, 16384], 64 / 8
   heads); ``decode_b1``: workload 0's latency; ``kv_write``: the pool write of the
   extend batch into an e4m3 pool; ``head_dim_256`` and ``head_dim_512``: decode and
-  extend at head dims 256 (workloads 5, 6) and 512 (7, 8). ``--headline-only`` skips all
-  of these.
+  extend at head dims 256 (workloads 5, 6) and 512 (7, 8); ``padded_head_dims``: the
+  extend batch at head dims 96 and 192 (workloads 9, 10) on the padded tiled kernel;
+  ``verify_fp8``: the verify batch over an e4m3 pool (workload 11). ``--headline-only``
+  skips all of these.
 
 ``value`` is whole-job throughput: algorithmic bytes of the K timed steps over
 the wall time between the two synchronisations. Warm-up is W untimed steps and
@@ -504,6 +506,10 @@ def main():
                                 "extend": _family(_measure(6, steps, args.warmup, 0), "extend_kernel", False)}
         line["head_dim_512"] = {"decode": _family(_measure(7, steps, args.warmup, 0), "any_kernel", True),
                                 "extend": _family(_measure(8, steps, args.warmup, 0), "any_kernel", False)}
+        # head dims without a tiled kernel of their own, padded onto the next one
+        line["padded_head_dims"] = {"d96_extend": _family(_measure(9, steps, args.warmup, 0), "extend_kernel", False),
+                                    "d192_extend": _family(_measure(10, steps, args.warmup, 0), "extend_kernel", False)}
+        line["verify_fp8"] = _family(_measure(11, steps, args.warmup, 0, kv_format="e4m3"), "splitkv_partial", True)
     print(json.dumps(line))
 
 
