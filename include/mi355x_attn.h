@@ -20,7 +20,9 @@
  * With page_size 1, table = req_to_token and row_index = req_pool_indices this
  * is SGLang's slot lookup; with a page table [B, max_pages] and row_index NULL it
  * is the paged layout [pages, page_size, Hkv, D] of the reference's kernels.
- * The table must cover every position below seq_lens[b].
+ * The table must cover every position below seq_lens[b]. A KV row (one slot's
+ * num_kv_heads x head_dim) must stay below 4 GiB of stride: the kernels multiply
+ * slots by it in 32 bits (MA_EUNSUPPORTED otherwise).
  *
  * Score scale is softmax_scale * k_scale; outputs are multiplied by v_scale
  * (sglang_restomod/attention/v100/tilelang/_paged_adapter.py:658,753-754).
