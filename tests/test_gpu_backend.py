@@ -111,10 +111,13 @@ def test_serving_sequence(kv_dtype):
 
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
-@pytest.mark.parametrize("hq,hkv,dim", [(8, 2, 64), (12, 2, 256), (8, 2, 96), (16, 4, 512)])
+@pytest.mark.parametrize("hq,hkv,dim", [(8, 2, 64), (12, 2, 256), (8, 2, 96), (8, 2, 192), (8, 2, 80),
+                                        (16, 4, 512)])
 def test_serving_sequence_head_dims(kv_dtype, hq, hkv, dim):
     """The same sequence at head dims 64 and 256 (the latter with the 27B model's
-    per-GPU head counts), and at 96 and 512, which run on the any-head-dim kernel."""
+    per-GPU head counts); at 96 and 192, whose extend runs on the padded tiled kernels
+    that skip their zero steps, and 80, padded without the skip; and at 512. Decode and
+    verify at the dims other than 64/128/256 run on the any-head-dim kernel."""
     _serving_sequence(kv_dtype, hq, hkv, dim)
 
 
