@@ -31,8 +31,10 @@ against the 8 TB/s HBM peak; ``roofline.traffic`` is the measured HBM bytes per
 launch of the dominant kernel, read from the committed counter summary
 (profiles/<kernel>__<workload>.traffic.md) when one exists for this workload.
 ``cpu_baseline`` times the torch-native SDPA restatement of the same workload
-(per-sequence gather + fp32 SDPA) on this host's cores. Prints exactly one
-JSON line.
+(per-sequence gather + fp32 SDPA) on this host's cores, over a bounded sample of its
+sequences (budgets: --cpu-seconds for the headline, --cpu-seconds-secondary for extend,
+fp8 decode, verify and B=1 decode, --cpu-seconds-tertiary for the rest); the KV write's
+is the numpy restatement of the pool write on one core. Prints exactly one JSON line.
 
     python bench.py --calibrate-copy 1024
 
@@ -71,6 +73,8 @@ def _parse():
                    help="CPU budget of the headline's torch-native baseline")
     p.add_argument("--cpu-seconds-secondary", type=float, default=10.0,
                    help="CPU budget of each other workload's baseline")
+    p.add_argument("--cpu-seconds-tertiary", type=float, default=5.0,
+                   help="CPU budget of the baselines of the head-dim, fp8 verify and KV write figures")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     return p.parse_args()
 
@@ -291,7 +295,39 @@ def _graph_us_per_call(index, calls=20, replays=20):
     return us
 
 
-def _measure_kv_write(steps, warmup):
+def _cpu_kv_write(k, v, loc, slots, k_scale, v_scale, budget_s, nbytes):
+    """The numpy restatement of the pool write (oracle.kv_write.set_kv_buffer, one core)
+    over the same K, V and slots: median of up to three timed calls."""
+    import numpy as np
+    import torch
+
+    from oracle import kv_write as KW
+
+    kb = k.cpu().view(torch.int16).numpy().view(np.uint16)  # bf16 bit patterns
+    vb = v.cpu().view(torch.int16).numpy().view(np.uint16)
+    lc = loc.cpu().numpy()
+    cache = np.zeros((slots,) + kb.shape[1:], dtype=np.uint8)
+
+    def call():
+        KW.set_kv_buffer(cache, lc, kb, "bf16", KW.E4M3, k_scale)
+        KW.set_kv_buffer(cache, lc, vb, "bf16", KW.E4M3, v_scale)
+
+    t0 = time.perf_counter()
+    call()
+    t = time.perf_counter() - t0
+    times = [t]
+    for _ in range(max(0, min(2, int(budget_s / max(t, 1e-3)) - 1))):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return {"value": round(nbytes / sec / 1e9, 5), "unit": "GB/s", "cores": 1, "kind": "port",
+            "seconds_per_call": round(sec, 6),
+            "sample": f"numpy restatement of the pool write (division in fp32, round to bf16, cast to e4m3) "
+                      f"over the whole batch, K and V, median of {len(times)} calls of {sec:.4g} s"}
+
+
+def _measure_kv_write(steps, warmup, cpu_seconds=0.0):
     """The pool write of an extend batch: the extend workload's new tokens (11,179 x 8 kv
     heads x 128, bf16 K and V) quantized into an e4m3 pool at shuffled slots."""
     import torch
@@ -314,11 +350,14 @@ def _measure_kv_write(steps, warmup):
     wall_ms, per = _time_gpu(fn, steps, warmup)
     nbytes = 2 * T * H * D * (2 + 1) + 8 * T
     ev = statistics.mean(per)
-    return {"workload": f"kv_write_t{T}_h{H}_d{D}_bf16_to_e4m3", "mode": "kv_write",
-            "ms_per_step": round(wall_ms, 5), "event_ms_mean": round(ev, 5),
-            "GBps": round(nbytes / (ev * 1e-3) / 1e9, 2),
-            "hbm_frac": round(nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes": nbytes}
+    res = {"workload": f"kv_write_t{T}_h{H}_d{D}_bf16_to_e4m3", "mode": "kv_write",
+           "ms_per_step": round(wall_ms, 5), "event_ms_mean": round(ev, 5),
+           "GBps": round(nbytes / (ev * 1e-3) / 1e9, 2),
+           "hbm_frac": round(nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "algorithmic_bytes": nbytes}
+    if cpu_seconds:
+        res["cpu_baseline"] = _cpu_kv_write(k, v, loc, slots, 0.9, 1.1, cpu_seconds, nbytes)
+    return res
 
 
 def _measure(index, steps, warmup, cpu_seconds, kv_format="e4m3"):
@@ -499,17 +538,19 @@ def main():
             # the same call replayed from a HIP graph: no host launch cost between its kernels
             obj["graph_us_per_call"] = round(_graph_us_per_call(0), 2)
             line["decode_b1"] = obj
-        line["kv_write"] = _measure_kv_write(steps, args.warmup)
+        ter = 0 if args.no_cpu_baseline else args.cpu_seconds_tertiary
+        line["kv_write"] = _measure_kv_write(steps, args.warmup, ter)
         # the other head dims of the reference's tuned configurations: 256 on the split-KV and
         # tiled extend kernels, 512 on the any-head-dim kernel
-        line["head_dim_256"] = {"decode": _family(_measure(5, steps, args.warmup, 0), "splitkv_partial", True),
-                                "extend": _family(_measure(6, steps, args.warmup, 0), "extend_kernel", False)}
-        line["head_dim_512"] = {"decode": _family(_measure(7, steps, args.warmup, 0), "any_kernel", True),
-                                "extend": _family(_measure(8, steps, args.warmup, 0), "any_kernel", False)}
+        line["head_dim_256"] = {"decode": _family(_measure(5, steps, args.warmup, ter), "splitkv_partial", True),
+                                "extend": _family(_measure(6, steps, args.warmup, ter), "extend_kernel", False)}
+        line["head_dim_512"] = {"decode": _family(_measure(7, steps, args.warmup, ter), "any_kernel", True),
+                                "extend": _family(_measure(8, steps, args.warmup, ter), "any_kernel", False)}
         # head dims without a tiled kernel of their own, padded onto the next one
-        line["padded_head_dims"] = {"d96_extend": _family(_measure(9, steps, args.warmup, 0), "extend_kernel", False),
-                                    "d192_extend": _family(_measure(10, steps, args.warmup, 0), "extend_kernel", False)}
-        line["verify_fp8"] = _family(_measure(11, steps, args.warmup, 0, kv_format="e4m3"), "splitkv_partial", True)
+        line["padded_head_dims"] = {"d96_extend": _family(_measure(9, steps, args.warmup, ter), "extend_kernel", False),
+                                    "d192_extend": _family(_measure(10, steps, args.warmup, ter), "extend_kernel", False)}
+        line["verify_fp8"] = _family(_measure(11, steps, args.warmup, ter, kv_format="e4m3"), "splitkv_partial",
+                                     True)
     print(json.dumps(line))
 
 
