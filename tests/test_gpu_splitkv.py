@@ -145,6 +145,18 @@ def test_decode_gqa_ratios(gpu, heads, heads_kv):
     _check_table_decode(q, k, v, table, seq, 1, out, 128 ** -0.5)
 
 
+@pytest.mark.parametrize("heads,heads_kv,dim", [(64, 4, 128), (12, 2, 256), (48, 2, 64)])
+def test_decode_persistent_merge_of_several_row_sets(gpu, heads, heads_kv, dim):
+    """The persistent split-KV path (no length hint) over sequences long enough that many
+    waves share each segment, at GQA groups whose rows fill more than one merge row set
+    (16 rows at D=128 and 6 at D=256: one merge workgroup per row set; 24 at D=64)."""
+    lengths = [5000, 7000, 300, 1]
+    q, k, v, table, seq = _synthetic(gpu, lengths, heads, heads_kv, dim=dim)
+    out = _ops().grouped_decode_forward(q, k, v, table, seq, softmax_scale=dim ** -0.5)
+    torch.cuda.synchronize()
+    _check_table_decode(q, k, v, table, seq, 1, out, dim ** -0.5)
+
+
 def test_decode_page_size_16_table(gpu):
     """The reference kernels' paged layout: [pages, 16, Hkv, D] through a page table."""
     lengths = [37, 53, 67, 200]
