@@ -190,17 +190,24 @@ def _time_gpu(fn, steps, warmup):
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
+    # the timed steps: back to back, with nothing else on the stream
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # the same number of steps again, each bracketed by HIP events on the launch stream
+    # (the kernels of one call; the event markers themselves add gaps between calls, so
+    # they stay out of the wall-clock loop above)
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         starts[i].record(stream)
         fn()
         ends[i].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     per = [s.elapsed_time(e) for s, e in zip(starts, ends)]  # ms, kernels of one call
     return wall / steps * 1e3, per
 
