@@ -178,8 +178,9 @@ def test_sweep_headdim_decode(dim, seed):
     assert_attn_close(_run_decode(c), _reference(c), what=f"decode D={dim} seed {seed}")
 
 
-# Head dims outside 64/128/256 run on the any-head-dim kernel (one wave per 16 rows, the
-# kernel padded to the next of 64/128/256/512): multiples of 16 across that range.
+# Head dims outside 64/128/256: decode and verify run on the any-head-dim kernel (one wave
+# per 16 rows, padded to the next of 64/128/256/512), extend up to 256 on the tiled extend
+# kernel of the next of 64/128/256 and above on the any-head-dim kernel.
 ANY_DIMS = [16, 48, 80, 96, 160, 192, 320, 448, 512]
 
 
@@ -188,6 +189,19 @@ ANY_DIMS = [16, 48, 80, 96, 160, 192, 320, 448, 512]
 def test_sweep_anydim_extend(dim, seed):
     c = _build(7000 + 10 * ANY_DIMS.index(dim) + seed, max_q=200, dim=dim)
     assert_attn_close(_run_extend(c), _reference(c), what=f"extend D={dim} seed {seed}")
+
+
+PADDED_DIMS = [d for d in range(16, 256, 16) if d not in (64, 128)]
+
+
+@pytest.mark.parametrize("dim", PADDED_DIMS)
+def test_sweep_every_padded_extend_dim(dim):
+    """Every head dim that runs padded on a tiled extend kernel (16-48 on the 64 kernel,
+    80-112 on 128, 144-240 on 256; 96 and 192 with their zero steps skipped). The seeded
+    cases span all four KV dtypes, fp16 and bf16 queries, windows and non-causal rows."""
+    seed = 9000 + dim
+    c = _build(seed, max_q=120, dim=dim)
+    assert_attn_close(_run_extend(c), _reference(c), what=f"extend D={dim}")
 
 
 @pytest.mark.parametrize("dim", ANY_DIMS)
