@@ -453,7 +453,8 @@ def _roofline(r, kernel, bound_hbm):
         "traffic": _traffic(kernel, r["profile_name"]),
         "kernel_ms": round(r["event_ms_mean"], 5),
         "timing": "HIP events on the launch stream around each call ("
-                  + (("any-head-dim kernel over key pieces + merge" if r["mode"] == "decode" else "any-head-dim kernel")
+                  + (("any-head-dim kernel; above 512 keys per row over key pieces + merge" if r["mode"] == "decode"
+                      else "any-head-dim kernel")
                      if kernel == "any_kernel" and bound_hbm
                      else "any-head-dim kernel, after the work-list plan" if kernel == "any_kernel"
                      else "split-KV partial + merge" if bound_hbm else "plan + extend kernel") + ")",
@@ -503,7 +504,8 @@ def main():
     cpu = 0 if args.no_cpu_baseline else args.cpu_seconds
     head = _measure(args.workload, args.steps, args.warmup, cpu, kv_format=args.kv_format)
     bound_hbm = head["mode"] != "extend"
-    kernel = "splitkv_partial" if bound_hbm else "extend_kernel"
+    kernel = (_decode_kernel(head) if head["mode"] == "decode"
+              else "splitkv_partial" if bound_hbm else "extend_kernel")
     line = {
         "metric": METRIC,
         "value": round(head["wall_GBps"] if bound_hbm else head["wall_TFLOPs"], 3),

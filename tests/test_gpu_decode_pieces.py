@@ -3,8 +3,9 @@ sequence's keys, then a merge kernel) against the float64 oracle and against the
 paths on the same inputs.
 
 * Head dims 64, 128 and 256: a decode whose split-KV work is small runs on the pieces when
-  the caller passes a host-known length bound (``max_seq_len_hint``); without one it runs
-  on the persistent split-KV kernel. Both are checked.
+  the caller passes a host-known length bound (``max_seq_len_hint``) above 512 keys (at or
+  below it, on one workgroup per row block); without one it runs on the persistent
+  split-KV kernel. All are checked.
 * Other head dims: with a workspace, a batch that leaves compute units idle is split into
   pieces; with a grid of one workgroup (``num_workgroups=1``) it is not. Both are checked,
   including a single sequence of 32k keys at head dims 96 and 512 (the case that ran on
@@ -94,7 +95,7 @@ def _check(c, out, what):
 
 
 TUNED = [
-    (1, 128, [512], 8, 4, torch.float16, -1),
+    (1, 128, [700], 8, 4, torch.float16, -1),
     (2, 128, [700, 0, 1, 33], 8, 8, torch.bfloat16, -1),
     (3, 128, [3000, 40], 2, 16, torch.float8_e4m3fn, 100),
     (4, 64, [900, 17], 4, 5, torch.float8_e5m2, -1),
@@ -119,7 +120,7 @@ def test_small_decode_runs_on_pieces_with_a_length_bound(seed, dim, lens, hkv, g
 ANY = [
     (11, 96, [2000, 5, 0], 4, 4, torch.bfloat16, -1),
     (12, 192, [800, 1200], 2, 8, torch.float8_e4m3fn, -1),
-    (13, 320, [333], 1, 3, torch.float16, 50),
+    (13, 320, [900], 1, 3, torch.float16, 50),
     (14, 512, [1024, 9], 4, 4, torch.float8_e5m2, -1),
     (15, 48, [4000], 8, 2, torch.bfloat16, -1),
 ]
