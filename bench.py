@@ -359,6 +359,7 @@ def _measure_kv_write(steps, warmup, cpu_seconds=0.0):
     ev = statistics.mean(per)
     res = {"workload": f"kv_write_t{T}_h{H}_d{D}_bf16_to_e4m3", "mode": "kv_write",
            "ms_per_step": round(wall_ms, 5), "event_ms_mean": round(ev, 5),
+           "event_ms_min": round(min(per), 5), "event_ms_median": round(statistics.median(per), 5),
            "GBps": round(nbytes / (ev * 1e-3) / 1e9, 2),
            "hbm_frac": round(nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            "algorithmic_bytes": nbytes}
@@ -388,6 +389,7 @@ def _measure(index, steps, warmup, cpu_seconds, kv_format="e4m3"):
         "ms_per_step": wall_ms,
         "event_ms_mean": ev_ms,
         "event_ms_min": min(per),
+        "event_ms_median": statistics.median(per),
         "algorithmic_bytes": nbytes,
         "algorithmic_flops": flops,
         "GBps": nbytes / (ev_ms * 1e-3) / 1e9,
@@ -452,6 +454,8 @@ def _roofline(r, kernel, bound_hbm):
         "frac": round(achieved / peak, 4),
         "traffic": _traffic(kernel, r["profile_name"]),
         "kernel_ms": round(r["event_ms_mean"], 5),
+        "kernel_ms_min": round(r["event_ms_min"], 5),
+        "kernel_ms_median": round(r["event_ms_median"], 5),
         "timing": "HIP events on the launch stream around each call ("
                   + (("any-head-dim kernel; above 512 keys per row over key pieces + merge" if r["mode"] == "decode"
                       else "any-head-dim kernel")
