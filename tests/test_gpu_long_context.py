@@ -1,12 +1,14 @@
-"""Long contexts through the tuned kernels against the float64 oracle.
+"""Long contexts and large batches through the tuned kernels against the float64 oracle.
 
 The split-KV decode and verify cut every (sequence, kv head, row group) into 32-key tiles
 (16 at D=256) and hand each wave of the persistent grid an equal range of the tile list,
 so a sequence of 131,072 keys is shared by about a hundred waves and merged from as many
 pieces; fp8 pools run the lazy rescale over the whole length. The extend kernel streams a
-64k-key prefix through every row tile. Each case is seeded; slots are a random
-permutation of the pool and the request rows are permuted inside a larger
-``req_to_token``.
+64k-key prefix through every row tile. A batch of 2,048 short sequences gives the decode
+16,384 segments and the extend a work list of 2,048 row tiles; a batch of 128 with a
+length bound of at most 512 keys runs the decode as one launch of the any-head-dim
+kernel. Each case is seeded; slots are a random permutation of the pool and the request
+rows are permuted inside a larger ``req_to_token``.
 """
 
 from __future__ import annotations
@@ -48,8 +50,8 @@ def _build(seed, prefix, ext, hkv, group, dim, kv, q_dtype):
     for b, n in enumerate(seq):
         r2t[rows[b], :n] = perm[off:off + n].to(torch.int32)
         off += n
-    print(f"[case] long seed={seed} D={dim} prefix={prefix} ext={ext} hkv={hkv} G={group} kv={kv} q={q_dtype}",
-          flush=True)
+    shape = f"prefix={prefix} ext={ext}" if B <= 4 else f"batch={B} keys={sum(seq)} rows={T}"
+    print(f"[case] long seed={seed} D={dim} {shape} hkv={hkv} G={group} kv={kv} q={q_dtype}", flush=True)
     return dict(q=q, k=k, v=v, r2t=r2t, rows=rows, seq=seq, prefix=prefix, ext=ext,
                 qsl=[0] + list(np.cumsum(ext)), ks=ks, vs=vs, scale=dim ** -0.5)
 
@@ -115,3 +117,33 @@ def test_extend_64k_prefix(gpu):
                                       softmax_scale=c["scale"], row_index=d["rows"])
     torch.cuda.synchronize()
     assert_attn_close(out, _reference(c), what="extend 64k prefix")
+
+
+def _ragged(seed, batch, lo, hi):
+    g = np.random.default_rng(seed)
+    return [int(x) for x in g.integers(lo, hi + 1, batch)]
+
+
+@pytest.mark.parametrize("batch,hint", [(2048, False), (128, True)])
+def test_decode_many_sequences(gpu, batch, hint):
+    """2,048 sequences without a length hint: the persistent kernel over 16,384 segments.
+    128 sequences with a hint of at most 512 keys: one launch of the any-head-dim kernel."""
+    lens = _ragged(106, batch, 1, 100 if batch > 512 else 500)
+    c = _build(106, [n - 1 for n in lens], [1] * len(lens), 8, 4, 128, torch.float16, torch.float16)
+    d = _device(c, gpu)
+    kw = {"max_seq_len_hint": max(lens)} if hint else {}
+    out = _ops().grouped_decode_forward(d["q"], d["k"], d["v"], d["r2t"], d["seq"], softmax_scale=c["scale"],
+                                        row_index=d["rows"], **kw)
+    torch.cuda.synchronize()
+    assert_attn_close(out, _reference(c), what=f"decode {batch} sequences hint={hint}")
+
+
+def test_extend_2048_sequences(gpu):
+    prefix = _ragged(107, 2048, 0, 100)
+    ext = _ragged(108, 2048, 1, 40)
+    c = _build(107, prefix, ext, 4, 4, 128, torch.bfloat16, torch.bfloat16)
+    d = _device(c, gpu)
+    out = _ops().paged_extend_forward(d["q"], d["k"], d["v"], d["r2t"], d["seq"], d["qsl"], d["pre"],
+                                      softmax_scale=c["scale"], row_index=d["rows"])
+    torch.cuda.synchronize()
+    assert_attn_close(out, _reference(c), what="extend 2048 sequences")
