@@ -38,9 +38,9 @@
 // Head dims 64, 128 and 256; the configuration measured and tuned is D = 128.
 //
 // Memory pipeline: K and V of up to S-1 tiles ahead are issued before a tile computes
-// (S = 3 for the one-row-group 16-bit kernels, 4 for the two-row-group and fp8 kernels,
-// 8 at D = 64); 16-bit KV waits for all of them before the compute, fp8 keeps them in
-// flight through it. Every load
+// (S = 2 for the one-row-group 16-bit kernels, 4 for the two-row-group and fp8 kernels,
+// 8 at D = 64); 16-bit KV at S >= 4 waits for all of them before the compute, the others
+// keep them in flight through it. Every load
 // instruction reads whole rows (1 KB: 64 / (row bytes / 16) rows) with the nontemporal
 // hint. K rows land in an AGPR ring and pass through a one-tile per-wave LDS staging
 // buffer into MFMA operand order when their tile is computed; V rows go straight to a
@@ -319,12 +319,13 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   // Pipeline stages: K of S tiles in a register ring, V of S tiles in an LDS ring. Each
   // step issues OPS vector memory instructions (one slot lookup, the V DMA, the K loads);
   // a wave can have at most 63 outstanding, which bounds S (kSMax). Fewer stages than
-  // the counter allows measured faster at D = 128 and 256: 3 for the one-row-group
-  // 16-bit kernels (4 measured 0.7-0.8% slower on bf16 decode, and 3 measured 1.9% slower
-  // on the two-row-group verify), 4 for the two-row-group and fp8 kernels (8 measured
-  // 6.6% slower on fp8 verify and 0.8-1.4% on fp8 decode). D = 64 keeps 8 (unmeasured).
+  // the counter allows measured faster at D = 128 and 256: 2 for the one-row-group
+  // 16-bit kernels (3 measured 1.2-1.5% slower on bf16 decode and 4 about 2% slower),
+  // 4 for the two-row-group 16-bit kernels (2 measured the same on verify, 3 1.9% slower)
+  // and for the fp8 kernels (8 measured 6.6% slower on fp8 verify and 0.8-1.4% on fp8
+  // decode, 2 much slower). D = 64 keeps 8 (unmeasured).
   constexpr int kSMax = 63 / OPS + 1;
-  constexpr int kSWant = (D == 64) ? 8 : (kFp8 || NB == 2) ? 4 : 3;
+  constexpr int kSWant = (D == 64) ? 8 : (kFp8 || NB == 2) ? 4 : 2;
   constexpr int S = kSMax < kSWant ? kSMax : kSWant;
   constexpr int A = 2 * S - 3;  // slots are looked up A tiles ahead of compute
   // Tiles kept in flight through a 16-bit tile's compute at S >= 4: none. Measured on
@@ -776,9 +777,9 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       // 16-bit KV at S >= 4 (the two-row-group kernels, and D = 64): every load issued so
       // far, the newest tile's included. Measured on decode and verify at S = 4, that is
       // 1.5-2.5% faster than keeping 1, 2 or S-1 tiles in flight through the compute: no
-      // DMA then writes the LDS ring while the tile's transposed V reads run. With S = 3
+      // DMA then writes the LDS ring while the tile's transposed V reads run. With S = 2
       // (the one-row-group 16-bit kernels) the wait for the slot above has already drained
-      // tile n, and the two newer tiles stay in flight. fp8 KV, half the bytes per tile:
+      // tile n, and tile n+1 stays in flight. fp8 KV, half the bytes per tile:
       // only tile n, so S-1 tiles stay in flight, which is 12% faster than waiting for all.
       wait_vm(std::integral_constant<int, (kFp8 || S < 4) ? (S - 1) * OPS : kInFlight16 * OPS>{});
       touch_k(ring[I]);
