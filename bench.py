@@ -19,8 +19,8 @@ extend TFLOP/s against the bf16 MFMA roofline), so one JSON line carries:
   extend batch into an e4m3 pool; ``head_dim_256`` and ``head_dim_512``: decode and
   extend at head dims 256 (workloads 5, 6) and 512 (7, 8); ``padded_head_dims``: the
   extend batch at head dims 96 and 192 (workloads 9, 10) on the padded tiled kernel;
-  ``verify_fp8``: the verify batch over an e4m3 pool (workload 11). ``--headline-only``
-  skips all of these.
+  ``verify_fp8`` and ``extend_fp8``: the verify and extend batches over an e4m3 pool
+  (workloads 11 and 12). ``--headline-only`` skips all of these.
 
 ``value`` is whole-job throughput: algorithmic bytes of the K timed steps over
 the wall time between the two synchronisations. Warm-up is W untimed steps and
@@ -564,6 +564,7 @@ def main():
                                     "d192_extend": _family(_measure(10, steps, args.warmup, ter), "extend_kernel", False)}
         line["verify_fp8"] = _family(_measure(11, steps, args.warmup, ter, kv_format="e4m3"), "splitkv_partial",
                                      True)
+        line["extend_fp8"] = _family(_measure(12, steps, args.warmup, ter, kv_format="e4m3"), "extend_kernel", False)
     print(json.dumps(line))
 
 

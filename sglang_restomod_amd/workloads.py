@@ -1,7 +1,7 @@
 """Seeded generators for the benchmark workloads: five at head dim 128 (0-4), two at
 head dim 256 (5, 6) and two at head dim 512 (7, 8); 9 and 10 are the extend batch of 8 at
-head dims 96 and 192 (parity cases of the any-head-dim kernel's extend); 11 is the
-verify batch over an fp8 pool.
+head dims 96 and 192 (on the padded tiled extend kernels); 11 and 12 are the verify and
+extend batches over an fp8 pool.
 
 Seeding scheme: one CPU ``torch.Generator`` per workload with seed = workload
 index. Draw order: lengths, slot permutation, then (on the target device,
@@ -50,6 +50,9 @@ WORKLOADS = {
              prefix=(0, 4096), extend=(256, 2048), heads=16, heads_kv=4, dim=192, dtype="fp16", kv="fp16"),
     11: dict(name="verify_b32_t4_p2k-16k_h64kv8_d128_fp8", mode="verify", batch=32, prefix=(2048, 16384),
              draft=4, heads=64, heads_kv=8, dim=128, dtype="bf16", kv="fp8"),
+    # workload 2's extend shape over an fp8 pool (its own seeded lengths, like workload 11)
+    12: dict(name="extend_b8_p0-4k_e256-2k_h40kv8_d128_fp8", mode="extend", batch=8,
+             prefix=(0, 4096), extend=(256, 2048), heads=40, heads_kv=8, dim=128, dtype="bf16", kv="fp8"),
 }
 
 _DT = {"fp16": torch.float16, "bf16": torch.bfloat16}

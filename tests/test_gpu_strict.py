@@ -8,8 +8,8 @@
 
 Workloads: decode B=1 (fp16), decode B=64 (bf16), fp8 decode B=128 in e4m3 and e5m2,
 verify B=32 x 4, extend B=8 (every row), the head-dim-256 and head-dim-512 decode and
-extend, the extend batch at head dims 96 (bf16) and 192 (fp16), and the verify batch
-over e4m3 and e5m2 pools.
+extend, the extend batch at head dims 96 (bf16) and 192 (fp16), and the verify and
+extend batches over e4m3 and e5m2 pools.
 """
 
 from __future__ import annotations
@@ -60,7 +60,7 @@ def _half_ulp(ref: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 CASES = [(0, "e4m3", False), (0, "e4m3", True), (1, "e4m3", False), (1, "e4m3", True), (3, "e4m3", False),
          (3, "e5m2", False), (4, "e4m3", False), (2, "e4m3", False), (5, "e4m3", False), (6, "e4m3", False),
          (7, "e4m3", False), (8, "e4m3", False), (9, "e4m3", False), (10, "e4m3", False), (11, "e4m3", False),
-         (11, "e5m2", False)]
+         (11, "e5m2", False), (12, "e4m3", False), (12, "e5m2", False)]
 
 
 @pytest.mark.parametrize("index,fmt,hint", CASES)
