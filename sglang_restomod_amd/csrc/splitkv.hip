@@ -38,16 +38,15 @@
 // Head dims 64, 128 and 256; the configuration measured and tuned is D = 128.
 //
 // Memory pipeline: K and V of up to S-1 tiles ahead are issued before a tile computes
-// (S = 2 for the one-row-group 16-bit kernels, 4 for the two-row-group and fp8 kernels,
-// 8 at D = 64); 16-bit KV at S >= 4 waits for all of them before the compute, the others
-// keep them in flight through it. Every load
-// instruction reads whole rows (1 KB: 64 / (row bytes / 16) rows) with the nontemporal
-// hint. K rows land in an AGPR ring and pass through a one-tile per-wave LDS staging
-// buffer into MFMA operand order when their tile is computed; V rows go straight to a
-// per-wave LDS ring by DMA (global_load_lds). Slots are looked up 2S-3 tiles ahead of compute. All of these are
-// issued as inline assembly and waited for with explicit counts. The issue cursor clamps
-// at the wave's last tile, so the pipelined loop has no data-dependent branches around
-// loads and the counts stay exact.
+// (S = 2 for 16-bit KV at D = 128 and 256, 4 for fp8 KV at D = 128); 16-bit KV at S >= 4
+// waits for all of them before the compute, the others keep them in flight through it.
+// Every load instruction reads whole rows (1 KB: 64 / (row bytes / 16) rows) with the
+// nontemporal hint, and lands them in a per-wave LDS ring by DMA (global_load_lds): V
+// rows in row-major order, K rows with their 16-byte chunks permuted by lane so that the
+// ring holds the swizzled layout the QK operand reads. Slots are looked up 2S-3 tiles
+// ahead of compute. All of these are issued as inline assembly and waited for with
+// explicit counts. The issue cursor clamps at the wave's last tile, so the pipelined
+// loop has no data-dependent branches around loads and the counts stay exact.
 
 #include <algorithm>
 #include <mutex>
@@ -66,8 +65,8 @@ constexpr int kWaves = 4;
 constexpr int kMaxRows = 32;  // 16 * NB, NB <= 2
 
 // Keys per tile: 32, and 16 for 16-bit KV at D = 256, whose 32-key tile would take 33 of
-// the 63 vector memory instructions a wave can have outstanding (leaving room for one
-// tile in flight); with 16 keys four stages fit.
+// the 63 vector memory instructions a wave can have outstanding, and 16 KB of K plus 16 KB
+// of V per wave and stage, one stage of LDS; with 16 keys two stages fit.
 template <int D, bool FP8>
 constexpr int kTileKeys() {
   return (D == 256 && !FP8) ? 16 : 32;
@@ -313,20 +312,23 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   constexpr int TB = kTile / 16;            // 16-key blocks per tile
   constexpr int kTS = kTile == 16 ? 4 : 5;  // log2(kTile)
   static_assert(TB == 2 || !kFp8, "fp8 V^T reads assume 32-key tiles");
-  constexpr int kStage = kTile * kRowB;     // bytes of one V tile
-  constexpr int kVL = kStage / 1024;        // 16-byte V loads per lane per tile
+  constexpr int kStage = kTile * kRowB;     // bytes of one K (or V) tile
+  constexpr int kVL = kStage / 1024;        // 16-byte K (or V) loads per lane per tile
   constexpr int OPS = 1 + 2 * kVL;          // vector memory instructions per pipeline step
-  // Pipeline stages: K of S tiles in a register ring, V of S tiles in an LDS ring. Each
-  // step issues OPS vector memory instructions (one slot lookup, the V DMA, the K loads);
-  // a wave can have at most 63 outstanding, which bounds S (kSMax). Fewer stages than
-  // the counter allows measured faster at D = 128 and 256: 2 for the one-row-group
+  // Pipeline stages: K and V of S tiles in per-wave LDS rings. Each step issues OPS
+  // vector memory instructions (one slot lookup, the V DMA, the K DMA); a wave can have
+  // at most 63 outstanding, which bounds S (kSMax), and the two rings of four waves must
+  // fit the CU's 160 KB of LDS (kSLds: 2 stages of 8 KB tiles, 5 of 4 KB tiles). Fewer
+  // stages than the counter allows measured faster: at D = 128, 2 for the one-row-group
   // 16-bit kernels (3 measured 1.2-1.5% slower on bf16 decode and 4 about 2% slower),
-  // 4 for the two-row-group 16-bit kernels (2 measured the same on verify, 3 1.9% slower)
-  // and for the fp8 kernels (8 measured 6.6% slower on fp8 verify and 0.8-1.4% on fp8
-  // decode, 2 much slower). D = 64 keeps 8 (unmeasured).
+  // and 4 for the fp8 kernels (8 measured 6.6% slower on fp8 verify and 0.8-1.4% on fp8
+  // decode, 2 much slower). The two-row-group 16-bit kernels measured the same on verify
+  // at 2 stages as at 4 when K still came through registers, where 4 fitted. 16-bit KV
+  // at D = 64 has fp8 D = 128's 4 KB tiles and takes its 4 stages (unmeasured).
   constexpr int kSMax = 63 / OPS + 1;
-  constexpr int kSWant = (D == 64) ? 8 : (kFp8 || NB == 2) ? 4 : 2;
-  constexpr int S = kSMax < kSWant ? kSMax : kSWant;
+  constexpr int kSLds = 160 * 1024 / (2 * kWaves * kStage);
+  constexpr int kSWant = kStage <= 4096 ? 4 : 2;
+  constexpr int S = std::min(std::min(kSMax, kSLds), kSWant);
   constexpr int A = 2 * S - 3;  // slots are looked up A tiles ahead of compute
   // Tiles kept in flight through a 16-bit tile's compute at S >= 4: none. Measured on
   // decode and verify with whole-row nontemporal loads, keeping 1, 2 or 3 in flight is
@@ -336,8 +338,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   static_assert(kVL >= 1 && 64 % kCPR == 0, "a V load covers whole rows");
 
   __shared__ __attribute__((aligned(16))) unsigned char vring[kWaves][S][kStage];
-  // K of the tile being computed, staged from the register ring into operand order
-  __shared__ __attribute__((aligned(16))) unsigned char kstage[kWaves][kStage];
+  __shared__ __attribute__((aligned(16))) unsigned char kring[kWaves][S][kStage];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     if constexpr (kFp8) return kCPR >= 8 ? ((t & 3) | ((t >> 2) & 4)) : (t & (kCPR - 1));
     else return (2 * t) & (kCPR - 2);
   };
-  // XOR swizzle of the 16-byte chunks of K row t in the staging buffer: the 16 rows an
+  // XOR swizzle of the 16-byte chunks of K row t in the K ring: the 16 rows an
   // operand read takes one chunk from land in 16 different 16-byte columns of a 256-byte
   // bank period (a row of kRowB bytes spans 256 / kRowB rows of a period).
   auto swzk = [](int t) -> int {
@@ -392,20 +393,13 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     return (t / kRowsPerPeriod) & (kCols - 1);
   };
 
-  // ---- per-tile K register ring (V goes to the LDS ring by DMA) ----
-  struct Raw {
-    u32x4 k[kVL];  // whole K rows: load x holds rows (64 / kCPR) x + lane / kCPR
-  };
-  Raw ring[S];
-  int sreg[S];
+  int sreg[S];  // slot lookups in flight, one per stage
 
   // The pipeline's vector memory instructions are issued as inline assembly and waited
   // for with explicit counts (wait_vm below): the compiler's own wait insertion cannot
-  // follow data across the register ring and the loop back edge, and it drains all
-  // outstanding loads before any LDS read once it has seen an LDS DMA. K rows load
-  // straight into AGPRs (MFMA operands), which the register allocator has no reason to
-  // copy before the wait; the build checks the generated code for any access to a
-  // register whose load is still in flight.
+  // follow the slot lookups across the loop back edge, and it drains all outstanding
+  // loads before any LDS read once it has seen an LDS DMA. The build checks the generated
+  // code for any access to a register whose load is still in flight.
   auto load_slot = [&](const Cursor& cu) __attribute__((always_inline)) -> int {
     const int key0 = cu.g.lo_min + cu.tile * kTile;
     const int pos = min(key0 + (lane & (kTile - 1)), cu.g.seq - 1);
@@ -422,10 +416,8 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     return (page << a.tt.page_shift) | (pos & ((1 << a.tt.page_shift) - 1));
   };
 
-  // V rows go straight to LDS stage `stage` (global_load_lds, issued first), then K rows
-  // into registers. Loads complete in issue order, so once the compiler has waited for
-  // this tile's K registers, its V rows are in LDS as well.
-  auto issue = [&](const Cursor& cu, int myslot, Raw& r, int stage) __attribute__((always_inline)) {
+  // V rows, then K rows, go straight to LDS stage `stage` of their rings (global_load_lds).
+  auto issue = [&](const Cursor& cu, int myslot, int stage) __attribute__((always_inline)) {
     const uint64_t hoff = (uint64_t)cu.h * (uint64_t)head_bytes;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)vring[wave][stage];
     // Byte offset of the row that load x of this lane reads (its slot times the row
@@ -446,26 +438,24 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + x * 1024);
       __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" MA_V_POLICY : : "s"(m0), "v"(src) : "memory", "m0");
     }
-    // K: whole rows per instruction, like V; lane chunk `pos` takes the row's chunk
-    // pos ^ swzk(tok), so that the staging copy below is a linear store
+    // K: whole rows per instruction, like V. The DMA writes lane chunks in lane order, so
+    // lane chunk `pos` fetching the row's chunk pos ^ swzk(tok) lands the swizzled layout.
+    const uint32_t kl0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)kring[wave][stage];
 #pragma unroll
     for (int x = 0; x < kVL; ++x) {
       const int tok = (64 / kCPR) * x + lane / kCPR;
       const int pos = lane % kCPR;
       const unsigned char MA_GLOBAL* kp = kbase + roff[x] + ((pos ^ swzk(tok)) << 4);
-      __asm__ volatile("global_load_dwordx4 %0, %1, off" MA_K_POLICY : "=a"(r.k[x]) : "v"(kp) : "memory");
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(kl0 + x * 1024);
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" MA_K_POLICY : : "s"(m0), "v"(kp) : "memory", "m0");
     }
   };
 
-  // Wait until at most N of this wave's vector memory instructions are outstanding, then
-  // mark `regs` as produced here so that no use of them is scheduled above the wait.
+  // Wait until at most N of this wave's vector memory instructions are outstanding; the
+  // memory clobber keeps the ring's LDS reads below the wait.
   auto wait_vm = [&](auto N_) __attribute__((always_inline)) {
     constexpr int N = decltype(N_)::value;
     __asm__ volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-  };
-  auto touch_k = [&](Raw& r) __attribute__((always_inline)) {
-#pragma unroll
-    for (int x = 0; x < kVL; ++x) __asm__ volatile("" : "+a"(r.k[x]));
   };
 
   // ---- per-segment state ----
@@ -573,13 +563,11 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     }
   };
 
-  auto compute = [&](const Cursor& cu, const Raw& r, int stage) __attribute__((always_inline)) {
+  auto compute = [&](const Cursor& cu, int stage) __attribute__((always_inline)) {
     const int tb0 = cu.g.lo_min + cu.tile * kTile;
     const unsigned char* vt = vring[wave][stage];
-    // ---- K operand: the tile's rows through the staging buffer into operand order ----
-    unsigned char* ks = kstage[wave];
-#pragma unroll
-    for (int x = 0; x < kVL; ++x) *reinterpret_cast<u32x4*>(ks + x * 1024 + lane * 16) = r.k[x];
+    // ---- K operand: the tile's rows from the K ring, unswizzled into operand order ----
+    const unsigned char* ks = kring[wave][stage];
     u32x4 kr[TB][KK];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
@@ -749,7 +737,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
       constexpr int W = ops_between(N + S - 1 - A, N - 1);
       wait_vm(std::integral_constant<int, W>{});
       __asm__ volatile("" : "+v"(sreg[RI]));
-      issue(ci, slot_of(ci, sreg[RI]), ring[RI], RI);
+      issue(ci, slot_of(ci, sreg[RI]), RI);
       cursor_next<kTS>(a, ci, count);
     }
   };
@@ -766,7 +754,7 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
     // K/V of tile n+S-1, once its slot lookup (A-S+1 steps ago) has landed
     wait_vm(std::integral_constant<int, OPS * (A - S + 1)>{});
     __asm__ volatile("" : "+v"(sreg[RI]));
-    issue(ci, slot_of(ci, sreg[RI]), ring[RI], RI);
+    issue(ci, slot_of(ci, sreg[RI]), RI);
     cursor_next<kTS>(a, ci, count);
     if (n < count) {
       if (cc.t == 0 || cc.tile == 0) {
@@ -774,16 +762,15 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
         piece_start_t = cc.t;
       }
       // tile n was issued at step n-S+1; the S-1 steps since then keep their loads in flight
-      // 16-bit KV at S >= 4 (the two-row-group kernels, and D = 64): every load issued so
-      // far, the newest tile's included. Measured on decode and verify at S = 4, that is
+      // 16-bit KV at S >= 4 (D = 64): every load issued so far, the newest tile's included.
+      // Measured on decode and verify at S = 4 (with K through registers), that was
       // 1.5-2.5% faster than keeping 1, 2 or S-1 tiles in flight through the compute: no
-      // DMA then writes the LDS ring while the tile's transposed V reads run. With S = 2
-      // (the one-row-group 16-bit kernels) the wait for the slot above has already drained
+      // DMA then writes the LDS rings while the tile's operand reads run. With S = 2
+      // (16-bit KV at D = 128 and 256) the wait for the slot above has already drained
       // tile n, and tile n+1 stays in flight. fp8 KV, half the bytes per tile:
       // only tile n, so S-1 tiles stay in flight, which is 12% faster than waiting for all.
       wait_vm(std::integral_constant<int, (kFp8 || S < 4) ? (S - 1) * OPS : kInFlight16 * OPS>{});
-      touch_k(ring[I]);
-      compute(cc, ring[I], I);
+      compute(cc, I);
       const bool seg_last = (cc.tile == cc.g.nt - 1);
       const bool range_last = (n == count - 1);
       if (seg_last || range_last) {
