@@ -379,9 +379,13 @@ __global__ __launch_bounds__(256, 1) void splitkv_partial(const SplitKVArgs args
   const int64_t head_bytes = a.kv_stride_head * kElt;
 
   // XOR swizzle of the 16-byte chunks of V row t in LDS (spreads the transposed reads
-  // over the banks); it stays below the row's chunk count
+  // over the banks); it stays below the row's chunk count. fp8: each 32-lane half of a
+  // transposed read takes one chunk of 16 rows, {0..7, 16..23} (+8 for the upper half);
+  // the row's index among them, (t & 7) | ((t >> 1) & 8), picks its 16-byte column of the
+  // 256-byte bank period (256 / kRowB rows share a period), so the 16 chunks fall in 16
+  // distinct columns.
   auto swz = [](int t) -> int {
-    if constexpr (kFp8) return kCPR >= 8 ? ((t & 3) | ((t >> 2) & 4)) : (t & (kCPR - 1));
+    if constexpr (kFp8) return (((t & 7) | ((t >> 1) & 8)) * kCPR) >> 4;
     else return (2 * t) & (kCPR - 2);
   };
   // XOR swizzle of the 16-byte chunks of K row t in the K ring: the 16 rows an
