@@ -38,8 +38,9 @@
 // Head dims 64, 128 and 256; the configuration measured and tuned is D = 128.
 //
 // Memory pipeline: K and V of up to S-1 tiles ahead are issued before a tile computes
-// (S = 2 for 16-bit KV at D = 128 and 256, 4 for fp8 KV at D = 128); 16-bit KV at S >= 4
-// waits for all of them before the compute, the others keep them in flight through it.
+// (S = 2 for 8 KB tiles: 16-bit KV at D = 128 and 256, fp8 at D = 256; 4 for smaller
+// ones: fp8 at D = 128, D = 64); 16-bit KV at S >= 4 waits for all of them before the
+// compute, the others keep them in flight through it.
 // Every load instruction reads whole rows (1 KB: 64 / (row bytes / 16) rows) with the
 // nontemporal hint, and lands them in a per-wave LDS ring by DMA (global_load_lds): V
 // rows in row-major order, K rows with their 16-byte chunks permuted by lane so that the
